@@ -1,0 +1,90 @@
+"""Launcher plumbing shared by the drop-in entry points.
+
+Each public function in this package follows the reference launcher's steps
+(e.g. attention_with_scores.py:239-333): validate shapes with the same
+asserts, default sm_scale to 1/sqrt(D), force innermost contiguity, allocate
+the outputs with torch on q's device, then make exactly one call into the
+gfx950 C ABI on torch's current stream.  Where the reference retries a Triton
+launch on an out-of-resources error, the HIP kernels have fixed, compile-time
+LDS budgets, so a failing call is reported at once as RuntimeError.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _native
+
+SUPPORTED_HEAD_DIMS = {16, 32, 64, 128}
+
+
+def maybe_contiguous(x: torch.Tensor) -> torch.Tensor:
+    """Innermost-contiguous view of x (flash.py:23-26)."""
+    return x.contiguous() if x.stride(-1) != 1 else x
+
+
+def _rows_aligned(x: torch.Tensor) -> bool:
+    # The kernels move 16-byte vectors: row starts must be 16-byte aligned.
+    return x.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in x.stride()[:3])
+
+
+def as_kernel_operand(x: torch.Tensor) -> torch.Tensor:
+    x = maybe_contiguous(x)
+    return x if _rows_aligned(x) else x.contiguous()
+
+
+@dataclass
+class Problem:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    B: int
+    H: int
+    M: int
+    N: int
+    D: int
+    Hk: int
+    sm_scale: float
+
+
+def check_device_inputs(q, k, v, dropout_p: float) -> None:
+    """Checks this build adds after the reference's own asserts."""
+    if dropout_p > 0.0:
+        raise NotImplementedError(
+            "flash_attn_with_score_amd: dropout_p > 0 is not supported by the gfx950 kernels")
+    assert q.dtype in _native.DTYPE_CODES, f"q.dtype must be float16 or bfloat16, got {q.dtype}"
+    assert k.dtype == q.dtype and v.dtype == q.dtype, "q, k, v must share one dtype"
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise RuntimeError("flash_attn_with_score_amd: q, k, v must be HIP device tensors")
+    assert k.device == q.device and v.device == q.device, "q, k, v must be on one device"
+    assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q, k, v must be (B, H, S, D)"
+    assert k.shape[0] == q.shape[0] and v.shape[0] == q.shape[0], "batch sizes must match"
+    assert v.shape[2] == k.shape[2], "k and v must have the same sequence length"
+
+
+def finish_problem(q, k, v, sm_scale) -> Problem:
+    B, H, M, D = q.shape
+    N = k.shape[2]
+    Hk = k.shape[1]
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    q, k, v = as_kernel_operand(q), as_kernel_operand(k), as_kernel_operand(v)
+    return Problem(q, k, v, B, H, M, N, D, Hk, float(sm_scale))
+
+
+def new_output(q: torch.Tensor) -> torch.Tensor:
+    o = torch.empty_like(q)
+    return o if _rows_aligned(o) and o.stride(-1) == 1 else torch.empty(
+        q.shape, dtype=q.dtype, device=q.device)
+
+
+def call(fn_name: str, q: torch.Tensor, *args) -> None:
+    """Invokes one C entry point on q's device and torch's current stream."""
+    lib = _native.load()
+    fn = getattr(lib, fn_name)
+    with torch.cuda.device(q.device):
+        stream = torch.cuda.current_stream(q.device).cuda_stream
+        rc = fn(*args, stream)
+    _native.check(lib, rc, fn_name)

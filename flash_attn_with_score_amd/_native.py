@@ -1,0 +1,154 @@
+"""ctypes binding of libfas.so, the gfx950 C ABI declared in include/fas.h.
+
+The library is loaded lazily, after torch (so it binds to the HIP runtime
+torch already mapped: both carry the soname libamdhip64.so.7).  There is no
+fallback: if the library is missing every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+ABI_VERSION = 1
+
+DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
+
+FAS_OK = 0
+FAS_ERR_INVALID = -1
+FAS_ERR_UNSUPPORTED = -2
+FAS_ERR_WORKSPACE = -3
+FAS_ERR_HIP = -4
+
+_I64x4 = ctypes.c_int64 * 4
+_I64x3 = ctypes.c_int64 * 3
+
+
+class AttnArgs(ctypes.Structure):
+    """Mirror of struct fas_attn_args (include/fas.h)."""
+
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("causal", ctypes.c_int32),
+        ("sm_scale", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
+        ("batch", ctypes.c_int64),
+        ("heads_q", ctypes.c_int64),
+        ("heads_k", ctypes.c_int64),
+        ("seqlen_q", ctypes.c_int64),
+        ("seqlen_k", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("q_stride", _I64x4),
+        ("k_stride", _I64x4),
+        ("v_stride", _I64x4),
+        ("out_stride", _I64x4),
+        ("lse", ctypes.c_void_p),
+        ("lse_stride", _I64x3),
+    ]
+
+
+def strides4(t: torch.Tensor):
+    return _I64x4(*t.stride())
+
+
+def strides3(t: torch.Tensor):
+    return _I64x3(*t.stride())
+
+
+def make_args(q, k, v, o, causal: bool, sm_scale: float, lse=None) -> AttnArgs:
+    B, H, M, D = q.shape
+    a = AttnArgs()
+    a.dtype = DTYPE_CODES[q.dtype]
+    a.causal = 1 if causal else 0
+    a.sm_scale = float(sm_scale)
+    a.batch, a.heads_q, a.seqlen_q, a.head_dim = B, H, M, D
+    a.heads_k, a.seqlen_k = k.shape[1], k.shape[2]
+    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
+    a.q_stride, a.k_stride, a.v_stride, a.out_stride = (
+        strides4(q), strides4(k), strides4(v), strides4(o))
+    if lse is not None:
+        a.lse = lse.data_ptr()
+        a.lse_stride = strides3(lse)
+    return a
+
+
+_P = ctypes.POINTER
+_SIGNATURES = {
+    "fas_abi_version": (ctypes.c_int, []),
+    "fas_last_error": (ctypes.c_char_p, []),
+    "fas_attention_with_scores": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x4, ctypes.c_void_p]),
+    "fas_attention_with_row_sum": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_with_col_sum": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_with_col_sum_sequential": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_with_softmax_col_sum": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_cross_token_qk_sum": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_cross_token_softmax_sum": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_cross_token_softmax_sum_buffered_workspace_bytes": (
+        ctypes.c_size_t, [_P(AttnArgs), ctypes.c_int64]),
+    "fas_attention_cross_token_softmax_sum_buffered": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, ctypes.c_void_p,
+                       ctypes.c_size_t, ctypes.c_void_p]),
+}
+
+EXPORTED_SYMBOLS = tuple(_SIGNATURES)
+
+
+def library_path() -> Path:
+    override = os.environ.get("FAS_LIBRARY")
+    if override:
+        return Path(override)
+    return Path(__file__).resolve().parent / "libfas.so"
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Returns the loaded library, raising if it is missing or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(
+                f"flash_attn_with_score_amd: native library {path} is not built; run "
+                "`python -c 'import __graft_entry__ as g; g.build()'` or "
+                "`python flash_attn_with_score_amd/csrc/build.py`")
+        lib = ctypes.CDLL(str(path))
+        for name, (restype, argtypes) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.fas_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libfas.so ABI version {version}, expected {ABI_VERSION}")
+        _lib = lib
+        return lib
+
+
+def last_error(lib) -> str:
+    msg = lib.fas_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(lib, rc: int, fn: str) -> None:
+    """Maps a negative fas_status to RuntimeError carrying the C message."""
+    if rc == FAS_OK:
+        return
+    msg = last_error(lib) or f"error code {rc}"
+    raise RuntimeError(f"{fn}: {msg}")

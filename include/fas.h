@@ -1,0 +1,157 @@
+/*
+ * fas.h -- C ABI of the MI355X (gfx950) fused flash-attention-forward family
+ * ("flash attention with scores").
+ *
+ * One entry point per reference launcher.  Each takes the shared attention
+ * description (fas_attn_args: q/k/v/out device pointers, element strides,
+ * sizes, dtype, causal flag, softmax scale) plus the side output of that
+ * variant, and enqueues the work asynchronously on the given HIP stream.
+ * Nothing here allocates device memory: every output, and the scratch buffer
+ * of the buffered cross-token variant, is owned by the caller.
+ *
+ * Conventions shared by every entry point (they restate the reference's
+ * Triton launchers; citations are to the reference checkout):
+ *   - q is (B, Hq, M, D); k and v are (B, Hk, N, D); out is like q.  Only the
+ *     innermost stride must be 1 (flash.py:23-26, maybe_contiguous); rows
+ *     must be 16-byte aligned (pointer and strides[0..2] multiples of 8).
+ *   - D in {16, 32, 64, 128}, Hq % Hk == 0; query head h reads KV head
+ *     h / (Hq/Hk) (attention_with_scores.py:57).
+ *   - Causal masking keeps (i, j) iff (N - M) + i >= j (bottom-right
+ *     aligned, attention_with_scores.py:136) except in the cross-token
+ *     QK-sum, which keeps i >= j (attention_cross_token_qk_sum.py:138).
+ *   - Softmax state is fp32, computed in base 2 on raw scores with
+ *     qk_scale = sm_scale * log2(e) (attention_with_scores.py:53-54,165-183).
+ *   - Query rows with no admissible key (causal, M > N) produce out = 0 and
+ *     a zero row sum (attention_with_scores.py:192-195).
+ *   - Column-type sums are per KV head: the Hq/Hk query heads of a group are
+ *     folded into one (B, Hk, *) vector (attention_with_col_sum.py:72,370).
+ *   - Sum outputs are fp32 and are zeroed by the entry point itself before
+ *     accumulation (the reference zero-fills with torch.zeros).
+ *
+ * Return value: FAS_OK (0) or a negative fas_status_t; fas_last_error()
+ * then returns a thread-local message naming the entry point and the cause.
+ */
+#ifndef FAS_H_
+#define FAS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FAS_ABI_VERSION 1
+
+typedef enum fas_dtype {
+  FAS_DTYPE_F16 = 0,
+  FAS_DTYPE_BF16 = 1
+} fas_dtype;
+
+typedef enum fas_status {
+  FAS_OK = 0,
+  FAS_ERR_INVALID = -1,     /* bad shape, pointer, stride or alignment */
+  FAS_ERR_UNSUPPORTED = -2, /* valid request this build does not implement */
+  FAS_ERR_WORKSPACE = -3,   /* caller-provided scratch too small */
+  FAS_ERR_HIP = -4          /* the HIP runtime rejected a launch */
+} fas_status;
+
+/* The attention problem shared by every entry point.  Strides are in
+ * elements, ordered (batch, head, row, dim); stride[3] must be 1. */
+typedef struct fas_attn_args {
+  int32_t dtype;   /* fas_dtype of q, k, v and out */
+  int32_t causal;  /* 0 or 1 */
+  float sm_scale;  /* softmax scale applied to q.k (1/sqrt(D) by default) */
+  int32_t reserved;
+  int64_t batch, heads_q, heads_k, seqlen_q, seqlen_k, head_dim;
+  const void* q;
+  const void* k;
+  const void* v;
+  void* out;
+  int64_t q_stride[4];
+  int64_t k_stride[4];
+  int64_t v_stride[4];
+  int64_t out_stride[4];
+  /* Optional natural-log LSE per query row, (B, Hq, M) fp32 with strides
+   * lse_stride (batch, head, row); NULL to skip.  The reference computes it
+   * (attention_with_scores.py:191-211) but no launcher returns it. */
+  float* lse;
+  int64_t lse_stride[3];
+} fas_attn_args;
+
+int fas_abi_version(void);
+
+/* Thread-local description of the last failure on this thread ("" if none). */
+const char* fas_last_error(void);
+
+/* Replaces attention_with_scores.py:214-333 (+ _fwd_kernel_with_scores
+ * :23-211).  scores is (B, Hq, M, N) in the input dtype with element strides
+ * scores_stride (innermost 1); it receives (q.k) * sm_scale, with masked
+ * positions (causal, upper triangle) written as 0.  The whole matrix is
+ * written by the kernel, so the caller need not zero it. */
+int fas_attention_with_scores(const fas_attn_args* a, void* scores,
+                              const int64_t scores_stride[4], void* stream);
+
+/* Replaces attention_with_row_sum.py:204-326 (+ kernel :22-202).
+ * row_sum is (B, Hq, M) fp32: sum over admissible keys of (q.k)*sm_scale. */
+int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum,
+                               const int64_t row_sum_stride[3], void* stream);
+
+/* Replaces attention_with_col_sum.py:297-419 (+ kernel :22-294): col_sum is
+ * (B, Hk, N) fp32, sum over queries and group heads of (q.k)*sm_scale.  Key
+ * tiles are visited in reverse order when causal, round-robin otherwise. */
+int fas_attention_with_col_sum(const fas_attn_args* a, float* col_sum,
+                               const int64_t col_sum_stride[3], void* stream);
+
+/* Replaces attention_with_col_sum_sequential.py:214-341 (+ kernel :23-211):
+ * same output as fas_attention_with_col_sum, round-robin key order. */
+int fas_attention_with_col_sum_sequential(const fas_attn_args* a, float* col_sum,
+                                          const int64_t col_sum_stride[3],
+                                          void* stream);
+
+/* Replaces attention_with_col_softmax_sum.py:274-401 (+ kernel :23-270):
+ * col_sum is (B, Hk, N) fp32, sum over queries and group heads of the final
+ * softmax weights P = exp(s - m) / l.  Two passes over K; the second pass
+ * visits key tiles in reverse order when causal. */
+int fas_attention_with_softmax_col_sum(const fas_attn_args* a, float* col_sum,
+                                       const int64_t col_sum_stride[3],
+                                       void* stream);
+
+/* Replaces attention_cross_token_qk_sum.py:255-408 (+ kernel :17-252):
+ * cross is (B, Hk, split) fp32, sum over queries i >= split of (q.k)*sm_scale
+ * for keys j < split.  Causal masking here (and for out) is top-left:
+ * i >= j.  0 < split <= N. */
+int fas_attention_cross_token_qk_sum(const fas_attn_args* a, int64_t split,
+                                     float* cross, const int64_t cross_stride[3],
+                                     void* stream);
+
+/* Replaces attention_cross_token_softmax_sum.py:735-863 (+ fused kernel
+ * :24-268): cross is (B, Hk, split) fp32, sum over queries i >= split of the
+ * softmax weights exp(s - m) / (l + 1e-12) for keys j < split. */
+int fas_attention_cross_token_softmax_sum(const fas_attn_args* a, int64_t split,
+                                          float* cross,
+                                          const int64_t cross_stride[3],
+                                          void* stream);
+
+/* Bytes of scratch fas_attention_cross_token_softmax_sum_buffered needs:
+ * the fp32 raw scores of the (i >= split, j < split) region,
+ * B * Hq * max(M - split, 0) * split * 4.  The reference sizes its buffer
+ * B * Hq * M * N * 4 (attention_cross_token_softmax_sum.py:704-705); only
+ * the region is ever re-read, so only the region is kept. */
+size_t fas_cross_token_softmax_sum_buffered_workspace_bytes(
+    const fas_attn_args* a, int64_t split);
+
+/* Replaces attention_cross_token_softmax_sum.py:639-732 (+ buffered kernel
+ * :434-636): same output as fas_attention_cross_token_softmax_sum, but pass 1
+ * stores the raw fp32 scores of the region in workspace and pass 2 reloads
+ * them instead of recomputing q.k. */
+int fas_attention_cross_token_softmax_sum_buffered(
+    const fas_attn_args* a, int64_t split, float* cross,
+    const int64_t cross_stride[3], void* workspace, size_t workspace_bytes,
+    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FAS_H_ */

@@ -1,0 +1,152 @@
+"""GPU parity of every entry point against the CPU oracle (small shapes).
+
+Each case draws seeded q/k/v on the CPU (oracle/inputs.py), runs the HIP
+entry point on the device, and compares output and side product with
+oracle/naive.py under the criteria of tests/tolerances.py.  Shapes cover
+MHA and GQA (group sizes 1, 2, 3, 7), every head dim, non-divisible
+lengths, M < N and M > N (rows with no admissible key under bottom-right
+causal masking), and split at 1, at tile edges and at N.
+"""
+from __future__ import annotations
+
+import sys
+
+import pytest
+import torch
+
+import flash_attn_with_score_amd as fas
+from oracle import inputs, naive
+from tests.tolerances import assert_out_close, assert_scores_close, assert_sum_close
+
+pytestmark = pytest.mark.gpu
+
+# (B, Hq, Hk, M, N, D)
+SHAPES = [
+    (1, 4, 4, 256, 256, 64),
+    (2, 4, 2, 200, 200, 128),
+    (1, 6, 2, 96, 160, 32),
+    (1, 2, 1, 160, 96, 16),
+    (1, 7, 1, 130, 130, 64),
+    (1, 3, 3, 64, 64, 128),
+    (1, 2, 2, 1, 77, 128),
+]
+
+PLAIN_EPS = [
+    "attention_with_scores",
+    "attention_with_row_sum",
+    "attention_with_col_sum",
+    "attention_with_col_sum_sequential",
+    "attention_with_softmax_col_sum",
+]
+CROSS_EPS = [
+    "attention_cross_token_qk_sum",
+    "attention_cross_token_softmax_sum",
+    "attention_cross_token_softmax_sum_buffered",
+]
+
+
+def _label(shape):
+    return "B{}H{}K{}M{}N{}D{}".format(*shape)
+
+
+def _run(ep, shape, dtype, causal, gpu, split=None, seed=0):
+    B, Hq, Hk, M, N, D = shape
+    print(f"[case] {ep} {_label(shape)} {dtype} causal={causal} split={split}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=seed)
+    fn = getattr(fas, ep)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    if split is None:
+        out, extra = fn(qd, kd, vd, causal=causal)
+    else:
+        out, extra = fn(qd, kd, vd, split, causal=causal)
+    torch.cuda.synchronize()
+    side = naive.ENTRY_POINT_OUTPUT[ep]
+    ref = naive.reference_forward(q, k, v, causal=causal, causal_offset=naive.ENTRY_POINT_OFFSET[ep],
+                                  split=split, want=("out", side))
+    assert out.dtype == dtype and out.shape == q.shape
+    assert_out_close(out, ref["out"])
+    if side == "scores":
+        assert extra.dtype == dtype and extra.shape == (B, Hq, M, N)
+        assert_scores_close(extra, ref["scores"])
+    else:
+        assert extra.dtype == torch.float32
+        assert_sum_close(extra, ref[side], side)
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=_label)
+@pytest.mark.parametrize("ep", PLAIN_EPS)
+def test_plain_entry_points(ep, shape, dtype, causal, gpu):
+    _run(ep, shape, dtype, causal, gpu)
+
+
+CROSS_CASES = [
+    ((1, 4, 4, 256, 256, 64), 100),
+    ((1, 4, 4, 256, 256, 64), 128),
+    ((1, 4, 4, 256, 256, 64), 1),
+    ((1, 4, 4, 256, 256, 64), 256),
+    ((2, 4, 2, 200, 200, 128), 77),
+    ((1, 7, 1, 130, 130, 64), 64),
+    ((1, 6, 2, 96, 160, 32), 150),
+    ((1, 2, 1, 160, 96, 16), 40),
+]
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", CROSS_CASES, ids=lambda c: f"{_label(c[0])}s{c[1]}")
+@pytest.mark.parametrize("ep", CROSS_EPS)
+def test_cross_entry_points(ep, case, dtype, causal, gpu):
+    shape, split = case
+    _run(ep, shape, dtype, causal, gpu, split=split)
+
+
+def test_scores_config2_shape(gpu):
+    """B1 H32 S1024 D128 fp16 causal (8 heads checked
+    against the oracle to bound CPU time; all heads checked for the causal
+    zero triangle)."""
+    B, H, M, D = 1, 32, 1024, 128
+    q, k, v = inputs.make_qkv(B, H, H, M, M, D, dtype=torch.float16, seed=0)
+    out, scores = fas.attention_with_scores(q.to(gpu), k.to(gpu), v.to(gpu), causal=True)
+    torch.cuda.synchronize()
+    upper = torch.triu(torch.ones(M, M, dtype=torch.bool, device=gpu), diagonal=1)
+    assert (scores[:, :, upper] == 0).all()
+    sel = [0, 5, 13, 31]
+    ref = naive.reference_forward(q[:, sel], k[:, sel], v[:, sel], causal=True, want=("out", "scores"))
+    assert_out_close(out[:, sel], ref["out"])
+    assert_scores_close(scores[:, sel], ref["scores"])
+
+
+def test_noncontiguous_inputs(gpu):
+    """(B, S, H, D) storage viewed as (B, H, S, D): strides are honoured."""
+    B, H, S, D = 1, 4, 192, 64
+    g = torch.Generator("cpu").manual_seed(3)
+    base = [torch.randn(B, S, H, D, generator=g).to(torch.float16) for _ in range(3)]
+    q, k, v = (t.transpose(1, 2) for t in base)
+    out, scores = fas.attention_with_scores(q.to(gpu), k.to(gpu), v.to(gpu), causal=True)
+    ref = naive.reference_forward(q, k, v, causal=True, want=("out", "scores"))
+    assert_out_close(out, ref["out"])
+    assert_scores_close(scores, ref["scores"])
+
+
+def test_cross_qk_out_buffers(gpu):
+    B, H, S, D, split = 1, 4, 256, 64, 96
+    q, k, v = inputs.make_qkv(B, H, H, S, S, D, dtype=torch.float16, seed=5)
+    out = torch.full((B, H, S, D), 7.0, dtype=torch.float16, device=gpu)
+    buf = torch.full((B, H, split), 3.0, dtype=torch.float32, device=gpu)
+    o, x = fas.attention_cross_token_qk_sum(q.to(gpu), k.to(gpu), v.to(gpu), split, causal=True,
+                                            out=out, cross_token_qk_out=buf)
+    assert o is out and x is buf
+    ref = naive.reference_forward(q, k, v, causal=True, causal_offset=0, split=split,
+                                  want=("out", "cross_qk"))
+    assert_out_close(o, ref["out"])
+    assert_sum_close(x, ref["cross_qk"], "cross_qk")
+
+
+def test_repeat_calls_consistent(gpu):
+    """Column sums via atomics vary only in the last bits between runs."""
+    q, k, v = inputs.make_qkv(1, 8, 2, 512, 512, 128, dtype=torch.bfloat16, seed=9, device=gpu)
+    _, a = fas.attention_with_softmax_col_sum(q, k, v, causal=True)
+    _, b = fas.attention_with_softmax_col_sum(q, k, v, causal=True)
+    assert_sum_close(a, b, "repeat")
