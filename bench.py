@@ -1,0 +1,278 @@
+"""Benchmark of the fused attention family on one MI355X.
+
+Default workload (the shape BASELINE.json's metric is quoted on):
+attention_with_scores, B=1, H=32, M=N=4096, D=128, fp16, causal.  A "step"
+is one call of the drop-in entry point over that batch with q/k/v already
+resident in HBM.  The line printed is the driver's JSON contract plus
+  roofline      dominant kernel vs MI355X peak (HBM for the score-writing
+                kernel, fp16 MFMA for the sum-only kernels), from HIP events
+                recorded on the stream the kernel runs on;
+  cpu_baseline  the CPU oracle (oracle/naive.py, a fp32 restatement of the
+                reference's naive attention) timed on a bounded sample of the
+                same workload on this host -- a reported baseline only;
+  secondary     the softmax column-sum kernel at the same shape against the
+                fp16 MFMA peak.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0        # MI355X HBM3E, GB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA, TFLOP/s
+
+METRIC = "fused attn TFLOP/s + scores-write GB/s, fp16 H32 S4096 D128 causal"
+
+# name -> (entry point, needs split, roofline bound, flop factor per pair
+#          (multiples of B*H*D per admissible pair), side product bytes fn)
+WORKLOADS = {
+    "scores": ("attention_with_scores", False, "hbm", 4),
+    "row_sum": ("attention_with_row_sum", False, "mfma", 4),
+    "col_sum": ("attention_with_col_sum", False, "mfma", 4),
+    "col_sum_sequential": ("attention_with_col_sum_sequential", False, "mfma", 4),
+    "col_softmax": ("attention_with_softmax_col_sum", False, "mfma", 6),
+    "cross_qk": ("attention_cross_token_qk_sum", True, "mfma", 4),
+    "cross_softmax": ("attention_cross_token_softmax_sum", True, "mfma", None),
+    "cross_softmax_buffered": ("attention_cross_token_softmax_sum_buffered", True, "hbm", None),
+}
+
+
+def pairs(M: int, N: int, causal: bool, offset: int) -> int:
+    """Admissible (query, key) pairs of one head: key j for query i iff
+    offset + i >= j when causal."""
+    if not causal:
+        return M * N
+    total = 0
+    for i in range(M):
+        total += max(0, min(N, offset + i + 1))
+    return total
+
+
+def cross_pairs(M: int, N: int, split: int, causal: bool, offset: int) -> int:
+    total = 0
+    for i in range(split, M):
+        hi = split if not causal else max(0, min(split, offset + i + 1))
+        total += hi
+    return total
+
+
+def work(name: str, B, H, Hk, M, N, D, causal, split, elem=2):
+    """(algorithmic FLOP, algorithmic HBM bytes) of one call."""
+    ep, _, _, fac = WORKLOADS[name]
+    off = 0 if name == "cross_qk" else N - M
+    P = pairs(M, N, causal, off)
+    qkvo = elem * (2 * B * H * M * D + 2 * B * Hk * N * D)
+    if name == "scores":
+        return 4 * B * H * D * P, qkvo + elem * B * H * M * N
+    if name == "row_sum":
+        return 4 * B * H * D * P, qkvo + 4 * B * H * M
+    if name in ("col_sum", "col_sum_sequential", "col_softmax"):
+        return fac * B * H * D * P, qkvo + 4 * B * Hk * N
+    Px = cross_pairs(M, N, split, causal, off)
+    if name == "cross_qk":
+        return 4 * B * H * D * P, qkvo + 4 * B * Hk * split
+    if name == "cross_softmax":
+        return 4 * B * H * D * P + 2 * B * H * D * Px, qkvo + 4 * B * Hk * split
+    # buffered: pass 2 reloads the region's fp32 scores instead of recomputing
+    region = 4 * B * H * max(M - split, 0) * split
+    return 4 * B * H * D * P, qkvo + 2 * region + 4 * B * Hk * split
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float) -> dict:
+    """Times the CPU oracle (oracle/naive.py, the checker) on whole heads of
+    the same workload until budget_s of work is done; the rate is scaled to
+    the heads actually computed."""
+    from oracle import inputs, naive
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0)
+    ep = WORKLOADS[name][0]
+    side = naive.ENTRY_POINT_OUTPUT[ep]
+    offset = naive.ENTRY_POINT_OFFSET[ep]
+    done = 0
+    t0 = time.perf_counter()
+    for h in range(H):
+        naive.reference_forward(q, k, v, causal=causal, causal_offset=offset, split=split,
+                                want=("out", side), heads=[h])
+        done += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    elapsed = time.perf_counter() - t0
+    flop, _ = work(name, B, H, Hk, M, N, D, causal, split)
+    flop_done = flop * done / H
+    return {
+        "value": round(flop_done / elapsed / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle/naive.py fp32 on {done} of {H} heads of {ep} at the bench shape "
+                  f"({elapsed:.1f} s; {cpu_model()}, os.cpu_count()={threads})",
+    }
+
+
+def make_call(fas, name, q, k, v, causal, split):
+    fn = getattr(fas, WORKLOADS[name][0])
+    if WORKLOADS[name][1]:
+        return lambda: fn(q, k, v, split, causal=causal)
+    return lambda: fn(q, k, v, causal=causal)
+
+
+def time_steps(call, steps: int, warmup: int):
+    """Wall time of `steps` calls, bracketed by synchronize, plus the average
+    device time per call from HIP events on torch's current stream (the
+    stream the entry points launch on)."""
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        call()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dev_ms = start.elapsed_time(end) / steps
+    return wall, dev_ms
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="scores")
+    ap.add_argument("--batch", type=int, default=1)
+    ap.add_argument("--heads", type=int, default=32)
+    ap.add_argument("--kv-heads", type=int, default=None)
+    ap.add_argument("--seqlen", type=int, default=4096)
+    ap.add_argument("--head-dim", type=int, default=128)
+    ap.add_argument("--split", type=int, default=None)
+    ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
+    ap.add_argument("--non-causal", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of CPU-oracle work for cpu_baseline (0 disables)")
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the path shards by (batch, KV-head group) with no communication, so N GPUs "
+              "run N independent copies -- no multi-GPU figure is produced.", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+
+    import flash_attn_with_score_amd as fas
+    from oracle import inputs
+
+    dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
+    B, H, M, D = args.batch, args.heads, args.seqlen, args.head_dim
+    N = M
+    Hk = args.kv_heads or H
+    causal = not args.non_causal
+    split = args.split
+    if WORKLOADS[args.workload][1] and split is None:
+        split = (3 * N) // 4
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0, device=dev)
+    call = make_call(fas, args.workload, q, k, v, causal, split)
+    wall, dev_ms = time_steps(call, args.steps, args.warmup)
+    flop, nbytes = work(args.workload, B, H, Hk, M, N, D, causal, split)
+    ms = wall * 1e3 / args.steps
+    tflops = flop / (ms * 1e-3) / 1e12
+    bound = WORKLOADS[args.workload][2]
+    if bound == "hbm":
+        achieved = nbytes / (dev_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4)}
+    else:
+        achieved = flop / (dev_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4)}
+    roof["traffic"] = None
+    roof["kernel_ms"] = round(dev_ms, 4)
+    roof["algorithmic_bytes"] = nbytes
+    roof["algorithmic_flop"] = flop
+
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic: q/k/v i.i.d. N(0,1) from a seeded CPU generator",
+        "config": {"workload": f"{WORKLOADS[args.workload][0]} B{B} H{H}/{Hk} "
+                               f"S{M} D{D} {args.dtype} {'causal' if causal else 'full'}"
+                               + (f" split{split}" if split else ""),
+                   "batch": B, "heads_q": H, "heads_k": Hk, "seqlen": M, "head_dim": D,
+                   "causal": causal, "split": split, "parallelism": "none (1 GPU)"},
+        "flop_convention": "4*B*H*D*(admissible pairs) (causal work); "
+                           "reference convention 4*B*H*M*N*D in tflops_ref_convention",
+        "tflops_ref_convention": round(4 * B * H * M * N * D / (ms * 1e-3) / 1e12, 2),
+        "hbm_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+    }
+    if args.workload == "scores":
+        line["scores_write_GBps"] = round(2 * B * H * M * N / (ms * 1e-3) / 1e9, 1)
+    line["roofline"] = roof
+
+    if not args.no_secondary and args.workload == "scores":
+        call2 = make_call(fas, "col_softmax", q, k, v, causal, None)
+        _, dev2 = time_steps(call2, max(5, args.steps // 2), max(2, args.warmup // 2))
+        flop2, _ = work("col_softmax", B, H, Hk, M, N, D, causal, None)
+        a2 = flop2 / (dev2 * 1e-3) / 1e12
+        line["secondary"] = {"workload": f"attention_with_softmax_col_sum B{B} H{H} S{M} D{D} "
+                                         f"{args.dtype} {'causal' if causal else 'full'}",
+                             "kernel_ms": round(dev2, 4), "achieved": round(a2, 1),
+                             "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(a2 / MFMA_F16_PEAK_TFLOPS, 4)}
+
+    del q, k, v
+    torch.cuda.synchronize()
+    if args.cpu_budget > 0:
+        line["cpu_baseline"] = cpu_baseline(args.workload, B, H, Hk, M, N, D, causal, split,
+                                            dtype, args.cpu_budget)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
