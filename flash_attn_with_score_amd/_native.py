@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -22,6 +22,16 @@ FAS_ERR_INVALID = -1
 FAS_ERR_UNSUPPORTED = -2
 FAS_ERR_WORKSPACE = -3
 FAS_ERR_HIP = -4
+
+# fas_variant (include/fas.h)
+VARIANT_SCORES = 0
+VARIANT_ROW_SUM = 1
+VARIANT_COL_SUM = 2
+VARIANT_COL_SUM_SEQUENTIAL = 3
+VARIANT_SOFTMAX_COL_SUM = 4
+VARIANT_CROSS_QK_SUM = 5
+VARIANT_CROSS_SOFTMAX_SUM = 6
+VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7
 
 _I64x4 = ctypes.c_int64 * 4
 _I64x3 = ctypes.c_int64 * 3
@@ -49,8 +59,6 @@ class AttnArgs(ctypes.Structure):
         ("k_stride", _I64x4),
         ("v_stride", _I64x4),
         ("out_stride", _I64x4),
-        ("lse", ctypes.c_void_p),
-        ("lse_stride", _I64x3),
     ]
 
 
@@ -62,7 +70,7 @@ def strides3(t: torch.Tensor):
     return _I64x3(*t.stride())
 
 
-def make_args(q, k, v, o, causal: bool, sm_scale: float, lse=None) -> AttnArgs:
+def make_args(q, k, v, o, causal: bool, sm_scale: float) -> AttnArgs:
     B, H, M, D = q.shape
     a = AttnArgs()
     a.dtype = DTYPE_CODES[q.dtype]
@@ -73,32 +81,29 @@ def make_args(q, k, v, o, causal: bool, sm_scale: float, lse=None) -> AttnArgs:
     a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
     a.q_stride, a.k_stride, a.v_stride, a.out_stride = (
         strides4(q), strides4(k), strides4(v), strides4(o))
-    if lse is not None:
-        a.lse = lse.data_ptr()
-        a.lse_stride = strides3(lse)
     return a
 
 
 _P = ctypes.POINTER
+_WS = [ctypes.c_void_p, ctypes.c_size_t]
 _SIGNATURES = {
     "fas_abi_version": (ctypes.c_int, []),
     "fas_last_error": (ctypes.c_char_p, []),
+    "fas_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _P(AttnArgs), ctypes.c_int64]),
     "fas_attention_with_scores": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x4, ctypes.c_void_p]),
     "fas_attention_with_row_sum": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
-    "fas_attention_with_col_sum": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_with_col_sum": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_with_col_sum_sequential": (
-        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_with_softmax_col_sum": (
-        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_cross_token_qk_sum": (
-        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_cross_token_softmax_sum": (
-        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
-    "fas_cross_token_softmax_sum_buffered_workspace_bytes": (
-        ctypes.c_size_t, [_P(AttnArgs), ctypes.c_int64]),
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_cross_token_softmax_sum_buffered": (
-        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, ctypes.c_void_p,
-                       ctypes.c_size_t, ctypes.c_void_p]),
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

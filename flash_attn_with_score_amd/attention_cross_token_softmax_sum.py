@@ -50,12 +50,10 @@ def attention_cross_token_softmax_sum_buffered(
     output = _common.new_output(p.q)
     cross = torch.empty((B, Hk, split), device=q.device, dtype=torch.float32)
     args = _native.make_args(p.q, p.k, p.v, output, causal, p.sm_scale)
-    lib = _native.load()
-    nbytes = int(lib.fas_cross_token_softmax_sum_buffered_workspace_bytes(ctypes.byref(args), split))
-    workspace = torch.empty((max(nbytes, 4) + 3) // 4, device=q.device, dtype=torch.float32)
+    ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_CROSS_SOFTMAX_SUM_BUFFERED, args, split,
+                                             q.device)
     _common.call("fas_attention_cross_token_softmax_sum_buffered", p.q, ctypes.byref(args),
-                 int(split), cross.data_ptr(), _native.strides3(cross), workspace.data_ptr(),
-                 workspace.numel() * 4)
+                 int(split), cross.data_ptr(), _native.strides3(cross), ws_ptr, ws_bytes)
     return output, cross
 
 
@@ -89,6 +87,8 @@ def attention_cross_token_softmax_sum(
     output = _common.new_output(p.q)
     cross = torch.empty((B, Hk, split), device=q.device, dtype=torch.float32)
     args = _native.make_args(p.q, p.k, p.v, output, causal, p.sm_scale)
+    ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_CROSS_SOFTMAX_SUM, args, split,
+                                             q.device)
     _common.call("fas_attention_cross_token_softmax_sum", p.q, ctypes.byref(args), int(split),
-                 cross.data_ptr(), _native.strides3(cross))
+                 cross.data_ptr(), _native.strides3(cross), ws_ptr, ws_bytes)
     return output, cross

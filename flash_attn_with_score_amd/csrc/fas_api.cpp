@@ -1,6 +1,6 @@
 // C ABI of the gfx950 fused attention family (declared in include/fas.h).
 //
-// Validates a request, packs the kernel parameter block and enqueues the
+// Validates a request, packs the kernel parameter blocks and enqueues the
 // launches on the caller's stream.  No device memory is allocated here and
 // nothing is synchronised.
 #include "fas.h"
@@ -10,6 +10,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <string>
 
 #include "fas_launch.hpp"
@@ -36,28 +37,50 @@ int hip_status(const char* fn, hipError_t e) {
 
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
-// Checks one (B, H, L, D)-shaped 16-bit tensor: innermost stride 1 and
-// 16-byte aligned rows, which the kernels' vector loads/stores require.
-int check_tensor(const char* fn, const char* name, const void* ptr, const int64_t* st) {
+constexpr int64_t kMaxSliceBytes = (int64_t)1 << 31;
+
+// Waves per forward workgroup at head dim 128 (4 or 8; FAS_FWD_WAVES).
+int fwd_waves() {
+  static const int w = [] {
+    const char* e = std::getenv("FAS_FWD_WAVES");
+    return (e != nullptr && std::atoi(e) == 4) ? 4 : 8;
+  }();
+  return w;
+}
+
+// Checks one (B, H, L, D)-shaped 16-bit tensor: innermost stride 1, 16-byte
+// aligned rows, and a (batch, head) slice addressable with 32-bit offsets
+// (including the tile overhang the kernels read past the last row).
+int check_tensor(const char* fn, const char* name, const void* ptr, const int64_t* st, int64_t rows,
+                 int64_t D) {
   if (ptr == nullptr) return fail(FAS_ERR_INVALID, fn, "%s is NULL", name);
-  if (st[3] != 1) return fail(FAS_ERR_INVALID, fn, "%s innermost stride must be 1 (got %lld)", name,
-                              (long long)st[3]);
+  if (st[3] != 1)
+    return fail(FAS_ERR_INVALID, fn, "%s innermost stride must be 1 (got %lld)", name,
+                (long long)st[3]);
   if (!aligned16(ptr) || st[0] % 8 || st[1] % 8 || st[2] % 8)
     return fail(FAS_ERR_INVALID, fn,
-                "%s rows must be 16-byte aligned (pointer and outer strides multiples of 8 elements)",
-                name);
+                "%s rows must be 16-byte aligned (pointer and outer strides multiples of 8)", name);
+  if (st[2] < D) return fail(FAS_ERR_INVALID, fn, "%s rows overlap (row stride < head_dim)", name);
+  if ((rows + 512) * st[2] * 2 >= kMaxSliceBytes)
+    return fail(FAS_ERR_UNSUPPORTED, fn, "%s (batch, head) slice exceeds 2 GiB", name);
   return FAS_OK;
 }
 
-// Fills the fields of the parameter block common to every variant.
-// top_left selects the cross-token QK-sum's causal alignment (i >= j)
-// instead of the bottom-right one ((N - M) + i >= j) used elsewhere.
-int fill_common(const char* fn, const fas_attn_args* a, fas::KParams* p, bool top_left) {
+uint32_t slice_bytes(int64_t rows, int64_t row_stride, int64_t D) {
+  return rows <= 0 ? 0u : (uint32_t)(((rows - 1) * row_stride + D) * 2);
+}
+
+struct Problem {
+  int B, H, Hk, G, M, N, D, dtype, causal;
+  float sm_scale;
+};
+
+// Sizes, dtype and flags only (no pointers): enough to size a workspace.
+int check_shape(const char* fn, const fas_attn_args* a, Problem* pr) {
   if (a == nullptr) return fail(FAS_ERR_INVALID, fn, "args is NULL");
   if (a->dtype != FAS_DTYPE_F16 && a->dtype != FAS_DTYPE_BF16)
     return fail(FAS_ERR_UNSUPPORTED, fn, "dtype %d is not fp16 (0) or bf16 (1)", (int)a->dtype);
-  if (a->causal != 0 && a->causal != 1)
-    return fail(FAS_ERR_INVALID, fn, "causal must be 0 or 1");
+  if (a->causal != 0 && a->causal != 1) return fail(FAS_ERR_INVALID, fn, "causal must be 0 or 1");
   const int64_t D = a->head_dim;
   if (D != 16 && D != 32 && D != 64 && D != 128)
     return fail(FAS_ERR_UNSUPPORTED, fn, "head_dim %lld not in {16, 32, 64, 128}", (long long)D);
@@ -66,83 +89,266 @@ int fill_common(const char* fn, const fas_attn_args* a, fas::KParams* p, bool to
   if (a->heads_q % a->heads_k != 0)
     return fail(FAS_ERR_INVALID, fn, "heads_q (%lld) is not a multiple of heads_k (%lld)",
                 (long long)a->heads_q, (long long)a->heads_k);
-  if (a->seqlen_q > (1 << 30) || a->seqlen_k > (1 << 30) || a->batch * a->heads_q > (1 << 30))
-    return fail(FAS_ERR_UNSUPPORTED, fn, "sizes exceed the 32-bit index range of the kernels");
+  if (a->seqlen_q > (1 << 28) || a->seqlen_k > (1 << 28) || a->batch * a->heads_q > (1 << 24))
+    return fail(FAS_ERR_UNSUPPORTED, fn, "sizes exceed the index range of the kernels");
   if (!std::isfinite(a->sm_scale)) return fail(FAS_ERR_INVALID, fn, "sm_scale is not finite");
-  const int64_t nrb = (a->seqlen_q + fas::kBMHost - 1) / fas::kBMHost;
-  if (nrb * a->batch * a->heads_q > 0xffffffffLL)
-    return fail(FAS_ERR_UNSUPPORTED, fn, "grid too large");
+  pr->B = (int)a->batch;
+  pr->H = (int)a->heads_q;
+  pr->Hk = (int)a->heads_k;
+  pr->G = pr->H / pr->Hk;
+  pr->M = (int)a->seqlen_q;
+  pr->N = (int)a->seqlen_k;
+  pr->D = (int)D;
+  pr->dtype = a->dtype;
+  pr->causal = a->causal;
+  pr->sm_scale = a->sm_scale;
+  return FAS_OK;
+}
 
-  *p = fas::KParams{};
-  p->q = static_cast<const uint16_t*>(a->q);
-  p->k = static_cast<const uint16_t*>(a->k);
-  p->v = static_cast<const uint16_t*>(a->v);
-  p->o = static_cast<uint16_t*>(a->out);
-  p->lse = a->lse;
-  p->sq0 = a->q_stride[0]; p->sq1 = a->q_stride[1]; p->sq2 = a->q_stride[2];
-  p->sk0 = a->k_stride[0]; p->sk1 = a->k_stride[1]; p->sk2 = a->k_stride[2];
-  p->sv0 = a->v_stride[0]; p->sv1 = a->v_stride[1]; p->sv2 = a->v_stride[2];
-  p->so0 = a->out_stride[0]; p->so1 = a->out_stride[1]; p->so2 = a->out_stride[2];
-  p->sl0 = a->lse_stride[0]; p->sl1 = a->lse_stride[1]; p->sl2 = a->lse_stride[2];
-  p->B = (int)a->batch;
-  p->H = (int)a->heads_q;
-  p->G = (int)(a->heads_q / a->heads_k);
-  p->M = (int)a->seqlen_q;
-  p->N = (int)a->seqlen_k;
-  p->split = 0;
-  p->causal = a->causal;
-  p->causal_off = top_left ? 0 : (int)(a->seqlen_k - a->seqlen_q);
-  p->order = fas::kOrderForward;
-  p->order2 = fas::kOrderForward;
-  p->nrb = (int)nrb;
-  p->sm_scale = a->sm_scale;
-  p->qk_scale = (float)((double)a->sm_scale * 1.4426950408889634);
-
-  if (a->batch * a->heads_q * a->seqlen_q == 0) return FAS_OK;  // nothing to read
+int check_args(const char* fn, const fas_attn_args* a, Problem* pr) {
   int rc;
-  if ((rc = check_tensor(fn, "q", a->q, a->q_stride))) return rc;
-  if ((rc = check_tensor(fn, "out", a->out, a->out_stride))) return rc;
-  if (a->seqlen_k > 0) {
-    if ((rc = check_tensor(fn, "k", a->k, a->k_stride))) return rc;
-    if ((rc = check_tensor(fn, "v", a->v, a->v_stride))) return rc;
+  if ((rc = check_shape(fn, a, pr))) return rc;
+  const int64_t D = pr->D;
+  if ((int64_t)pr->B * pr->H * pr->M == 0) return FAS_OK;  // nothing is read
+  if ((rc = check_tensor(fn, "q", a->q, a->q_stride, pr->M, D))) return rc;
+  if ((rc = check_tensor(fn, "out", a->out, a->out_stride, pr->M, D))) return rc;
+  if (pr->N > 0) {
+    if ((rc = check_tensor(fn, "k", a->k, a->k_stride, pr->N, D))) return rc;
+    if ((rc = check_tensor(fn, "v", a->v, a->v_stride, pr->N, D))) return rc;
   }
   return FAS_OK;
 }
 
-bool empty_launch(const fas::KParams& p) { return (int64_t)p.B * p.H * p.M == 0; }
+// Fills the forward parameter block.  top_left selects the cross-token
+// QK-sum's causal alignment (i >= j) instead of (N - M) + i >= j.
+fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_left, int rows_per_block) {
+  fas::FwdParams p{};
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<uint16_t*>(a->out);
+  p.sq0 = a->q_stride[0]; p.sq1 = a->q_stride[1]; p.sq2 = a->q_stride[2];
+  p.sk0 = a->k_stride[0]; p.sk1 = a->k_stride[1]; p.sk2 = a->k_stride[2];
+  p.sv0 = a->v_stride[0]; p.sv1 = a->v_stride[1]; p.sv2 = a->v_stride[2];
+  p.so0 = a->out_stride[0]; p.so1 = a->out_stride[1]; p.so2 = a->out_stride[2];
+  p.q_bytes = slice_bytes(pr.M, p.sq2, pr.D);
+  p.o_bytes = slice_bytes(pr.M, p.so2, pr.D);
+  p.k_bytes = slice_bytes(pr.N, p.sk2, pr.D);
+  p.v_bytes = slice_bytes(pr.N, p.sv2, pr.D);
+  p.qneg = pr.sm_scale < 0.f ? 0x80008000u : 0u;
+  p.B = pr.B;
+  p.H = pr.H;
+  p.G = pr.G;
+  p.M = pr.M;
+  p.N = pr.N;
+  p.causal = pr.causal;
+  p.causal_off = top_left ? 0 : pr.N - pr.M;
+  p.nrb = (pr.M + rows_per_block - 1) / rows_per_block;
+  p.sm_scale = std::fabs(pr.sm_scale);
+  p.qk_scale = (float)((double)std::fabs(pr.sm_scale) * 1.4426950408889634);
+  return p;
+}
 
-int set_aux(const char* fn, fas::KParams* p, float* aux, const int64_t* st, const char* name) {
-  if (aux == nullptr) return fail(FAS_ERR_INVALID, fn, "%s is NULL", name);
+int run_fwd(const char* fn, fas::FwdParams& p, const Problem& pr, int mode, int waves, void* stream) {
+  if (p.nrb == 0 || (int64_t)pr.B * pr.H == 0) return FAS_OK;
+  return hip_status(fn, fas::launch_fwd(p, mode, pr.dtype, pr.D, waves,
+                                        static_cast<hipStream_t>(stream)));
+}
+
+int check_out3(const char* fn, const char* name, const float* out, const int64_t* st) {
+  if (out == nullptr) return fail(FAS_ERR_INVALID, fn, "%s is NULL", name);
   if (st == nullptr) return fail(FAS_ERR_INVALID, fn, "%s strides are NULL", name);
-  p->aux = aux;
-  p->sa0 = st[0];
-  p->sa1 = st[1];
-  p->sa2 = st[2];
   return FAS_OK;
 }
 
-int zero_aux(const char* fn, const fas::KParams& p, int64_t n1, int64_t n2, hipStream_t s) {
-  return hip_status(fn, fas::launch_fill_zero(p.aux, p.sa0, p.sa1, p.sa2, p.B, n1, n2, s));
+int zero_out3(const char* fn, float* out, const int64_t* st, int64_t n0, int64_t n1, int64_t n2,
+              void* stream) {
+  return hip_status(fn, fas::launch_fill_zero(out, st[0], st[1], st[2], n0, n1, n2,
+                                              static_cast<hipStream_t>(stream)));
 }
 
-int check_split(const char* fn, const fas_attn_args* a, int64_t split) {
-  if (!(split > 0 && split <= a->seqlen_k))
-    return fail(FAS_ERR_INVALID, fn, "split %lld outside (0, %lld]", (long long)split,
-                (long long)a->seqlen_k);
+// ---------------------------------------------------------------- workspace
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct Workspace {
+  size_t lse = 0, part = 0, bsum = 0, region = 0, total = 0;  // byte offsets / total
+  bool has_lse = false, has_part = false, has_bsum = false, has_region = false;
+};
+
+// Column count of a variant's side output.
+int64_t ncols_of(int variant, const Problem& pr, int64_t split) {
+  switch (variant) {
+    case FAS_VARIANT_CROSS_QK_SUM:
+    case FAS_VARIANT_CROSS_SOFTMAX_SUM:
+    case FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED: return split;
+    default: return pr.N;
+  }
+}
+
+Workspace layout(int variant, const Problem& pr, int64_t split) {
+  Workspace w;
+  size_t off = 0;
+  const int64_t ncols = ncols_of(variant, pr, split);
+  const bool softmax = variant == FAS_VARIANT_SOFTMAX_COL_SUM ||
+                       variant == FAS_VARIANT_CROSS_SOFTMAX_SUM ||
+                       variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED;
+  const bool raw = variant == FAS_VARIANT_COL_SUM || variant == FAS_VARIANT_COL_SUM_SEQUENTIAL ||
+                   variant == FAS_VARIANT_CROSS_QK_SUM;
+  if (softmax) {
+    w.has_lse = true;
+    w.lse = off;
+    off += align256((size_t)pr.B * pr.H * pr.M * 4);
+    if (pr.G > 1) {
+      w.has_part = true;
+      w.part = off;
+      off += align256((size_t)pr.B * pr.H * ncols * 4);
+    }
+  }
+  if (variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED) {
+    w.has_region = true;
+    w.region = off;
+    const int64_t rows = pr.M > split ? pr.M - split : 0;
+    off += align256((size_t)pr.B * pr.H * rows * split * 4);
+  }
+  if (raw) {
+    const int64_t row_lo = variant == FAS_VARIANT_CROSS_QK_SUM ? split : 0;
+    const int64_t rows = pr.M > row_lo ? pr.M - row_lo : 0;
+    const int64_t nblk = (rows + 63) / 64;
+    w.has_bsum = true;
+    w.bsum = off;
+    off += align256((size_t)pr.B * pr.Hk * (nblk + 1) * pr.D * 4);
+  }
+  w.total = off;
+  return w;
+}
+
+int check_workspace(const char* fn, const Workspace& w, void* ws, size_t bytes) {
+  if (w.total == 0) return FAS_OK;
+  if (ws == nullptr || bytes < w.total)
+    return fail(FAS_ERR_WORKSPACE, fn, "workspace of %zu bytes needed, %zu given", w.total, bytes);
+  if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return fail(FAS_ERR_INVALID, fn, "workspace must be 256-byte aligned");
   return FAS_OK;
 }
 
-using Launcher = hipError_t (*)(const fas::KParams&, int, int, hipStream_t);
+template <class T>
+T* at(void* ws, size_t off) {
+  return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
+}
 
-// Column-type sum over (B, Hk, n2): zero, then launch.
-int run_col(const char* fn, const fas_attn_args* a, float* out, const int64_t* st, int64_t n2,
-            fas::KParams* p, Launcher launch, void* stream) {
+// ---------------------------------------------------------------- variants
+
+// Raw-score column sums (col_sum, col_sum_sequential, cross_qk).
+int run_raw(const char* fn, int variant, const fas_attn_args* a, int64_t split, float* out,
+            const int64_t* st, void* ws, size_t ws_bytes, void* stream) {
+  Problem pr;
   int rc;
-  if ((rc = set_aux(fn, p, out, st, "sum output"))) return rc;
+  if ((rc = check_args(fn, a, &pr))) return rc;
+  const bool cross = variant == FAS_VARIANT_CROSS_QK_SUM;
+  if (cross && !(split > 0 && split <= pr.N))
+    return fail(FAS_ERR_INVALID, fn, "split %lld outside (0, %d]", (long long)split, pr.N);
+  if ((rc = check_out3(fn, "sum output", out, st))) return rc;
+  const int64_t ncols = ncols_of(variant, pr, split);
+  if ((int64_t)pr.B * pr.Hk * ncols == 0) {
+    fas::FwdParams p = fwd_params(a, pr, cross, fas::fwd_rows_per_block(pr.D, fwd_waves()));
+    return run_fwd(fn, p, pr, fas::kFwdPlain, fwd_waves(), stream);
+  }
+  const Workspace w = layout(variant, pr, split);
+  if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
+
+  // Attention output.
+  const int waves = fwd_waves();
+  fas::FwdParams p = fwd_params(a, pr, cross, fas::fwd_rows_per_block(pr.D, waves));
+  if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, waves, stream))) return rc;
+  if (pr.M == 0) return zero_out3(fn, out, st, pr.B, pr.Hk, ncols, stream);
+
+  fas::RawParams r{};
+  r.q = p.q;
+  r.k = p.k;
+  r.bsum = at<float>(ws, w.bsum);
+  r.out = out;
+  r.sq0 = p.sq0; r.sq1 = p.sq1; r.sq2 = p.sq2;
+  r.sk0 = p.sk0; r.sk1 = p.sk1; r.sk2 = p.sk2;
+  r.so0 = st[0]; r.so1 = st[1]; r.so2 = st[2];
+  r.B = pr.B; r.H = pr.H; r.G = pr.G; r.Hk = pr.Hk; r.M = pr.M; r.N = pr.N; r.D = pr.D;
+  r.row_lo = cross ? (int)split : 0;
+  r.nblk = pr.M > r.row_lo ? (pr.M - r.row_lo + 63) / 64 : 0;
+  r.ncols = (int)ncols;
+  r.causal = pr.causal;
+  r.causal_off = pr.N - pr.M;
+  // Cross-token sums see every (i >= split, j < split) pair under the
+  // top-left mask, so only the bottom-right causal column sum needs the
+  // per-key suffix.
+  const bool suffix = !cross && pr.causal;
+  r.nextra = suffix && r.causal_off > 0 ? (std::min(r.ncols, r.causal_off) + 63) / 64 : 0;
+  r.sm_scale = pr.sm_scale;
+  return hip_status(fn, fas::launch_rawsum(r, pr.dtype, suffix, static_cast<hipStream_t>(stream)));
+}
+
+// Softmax-weight column sums (softmax col sum, cross softmax, buffered).
+int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t split, float* out,
+                const int64_t* st, void* ws, size_t ws_bytes, void* stream) {
+  Problem pr;
+  int rc;
+  if ((rc = check_args(fn, a, &pr))) return rc;
+  const bool cross = variant != FAS_VARIANT_SOFTMAX_COL_SUM;
+  const bool buffered = variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED;
+  if (cross && !(split > 0 && split <= pr.N))
+    return fail(FAS_ERR_INVALID, fn, "split %lld outside (0, %d]", (long long)split, pr.N);
+  if ((rc = check_out3(fn, "sum output", out, st))) return rc;
+  const int64_t ncols = ncols_of(variant, pr, split);
+  const Workspace w = layout(variant, pr, split);
+  if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
+
+  const int waves = buffered ? 8 : fwd_waves();
+  fas::FwdParams p = fwd_params(a, pr, false, fas::fwd_rows_per_block(pr.D, waves));
+  p.lse2 = at<float>(ws, w.lse);
+  if (buffered) {
+    p.region = at<float>(ws, w.region);
+    p.split = (int)split;
+    p.vec_region = (split % 4 == 0) ? 1 : 0;
+  }
+  if ((rc = run_fwd(fn, p, pr, buffered ? fas::kFwdRegion : fas::kFwdPlain, waves, stream)))
+    return rc;
+  if ((int64_t)pr.B * pr.Hk * ncols == 0) return FAS_OK;
+  if ((int64_t)pr.B * pr.H * pr.M == 0) return zero_out3(fn, out, st, pr.B, pr.Hk, ncols, stream);
+
+  fas::ColsmParams c{};
+  c.q = p.q;
+  c.k = p.k;
+  c.lse2 = p.lse2;
+  c.region = p.region;
+  c.sq0 = p.sq0; c.sq1 = p.sq1; c.sq2 = p.sq2;
+  c.sk0 = p.sk0; c.sk1 = p.sk1; c.sk2 = p.sk2;
+  c.q_bytes = p.q_bytes;
+  c.k_bytes = p.k_bytes;
+  c.qneg = p.qneg;
+  c.B = pr.B; c.H = pr.H; c.G = pr.G; c.M = pr.M; c.N = pr.N;
+  c.row_lo = cross ? (int)split : 0;
+  c.ncols = (int)ncols;
+  c.split = (int)split;
+  c.causal = pr.causal;
+  c.causal_off = pr.N - pr.M;
+  c.nkb = (int)((ncols + 255) / 256);
+  c.qk_scale = p.qk_scale;
+  float* part = nullptr;
+  if (pr.G > 1) {
+    part = at<float>(ws, w.part);
+    c.out = part;
+    c.so0 = (int64_t)pr.H * ncols;
+    c.so1 = ncols;
+    c.so2 = 1;
+  } else {
+    c.out = out;
+    c.so0 = st[0]; c.so1 = st[1]; c.so2 = st[2];
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if ((rc = zero_aux(fn, *p, a->heads_k, n2, s))) return rc;
-  if (empty_launch(*p)) return FAS_OK;
-  return hip_status(fn, launch(*p, a->dtype, (int)a->head_dim, s));
+  if ((rc = hip_status(fn, fas::launch_colsm(c, pr.dtype, pr.D, buffered, s)))) return rc;
+  if (pr.G > 1)
+    return hip_status(fn, fas::launch_group_reduce(part, out, st[0], st[1], st[2], pr.B, pr.Hk,
+                                                   pr.G, (int)ncols, s));
+  return FAS_OK;
 }
 
 }  // namespace
@@ -153,123 +359,98 @@ int fas_abi_version(void) { return FAS_ABI_VERSION; }
 
 const char* fas_last_error(void) { return g_last_error.c_str(); }
 
-int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_t scores_stride[4],
+size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
+  Problem pr;
+  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED)
+    return (size_t)-1;
+  if (check_shape("fas_workspace_bytes", a, &pr)) return (size_t)-1;
+  const bool has_split = variant == FAS_VARIANT_CROSS_QK_SUM ||
+                         variant == FAS_VARIANT_CROSS_SOFTMAX_SUM ||
+                         variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED;
+  if (has_split && !(split > 0 && split <= pr.N)) return (size_t)-1;
+  return layout(variant, pr, has_split ? split : 0).total;
+}
+
+int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_t st[4],
                               void* stream) {
   static const char* fn = "fas_attention_with_scores";
-  fas::KParams p;
+  Problem pr;
   int rc;
-  if ((rc = fill_common(fn, a, &p, false))) return rc;
-  if (empty_launch(p) || a->seqlen_k == 0) return FAS_OK;
-  if (scores == nullptr || scores_stride == nullptr)
-    return fail(FAS_ERR_INVALID, fn, "scores is NULL");
-  if (scores_stride[3] != 1) return fail(FAS_ERR_INVALID, fn, "scores innermost stride must be 1");
+  if ((rc = check_args(fn, a, &pr))) return rc;
+  if ((int64_t)pr.B * pr.H * pr.M == 0) return FAS_OK;
+  if (scores == nullptr || st == nullptr) return fail(FAS_ERR_INVALID, fn, "scores is NULL");
+  if (st[3] != 1) return fail(FAS_ERR_INVALID, fn, "scores innermost stride must be 1");
   if (reinterpret_cast<uintptr_t>(scores) & 1u)
     return fail(FAS_ERR_INVALID, fn, "scores is not 2-byte aligned");
+  const int waves = fwd_waves();
+  const int bm = fas::fwd_rows_per_block(pr.D, waves);
+  if ((int64_t)bm * st[2] * 2 >= kMaxSliceBytes)
+    return fail(FAS_ERR_UNSUPPORTED, fn, "score rows too long for 32-bit offsets");
+  fas::FwdParams p = fwd_params(a, pr, false, bm);
   p.scores = static_cast<uint16_t*>(scores);
-  p.ss0 = scores_stride[0];
-  p.ss1 = scores_stride[1];
-  p.ss2 = scores_stride[2];
-  p.vec_scores = aligned16(scores) && p.ss0 % 8 == 0 && p.ss1 % 8 == 0 && p.ss2 % 8 == 0;
-  return hip_status(fn, fas::launch_scores(p, a->dtype, (int)a->head_dim,
-                                           static_cast<hipStream_t>(stream)));
+  p.ss0 = st[0];
+  p.ss1 = st[1];
+  p.ss2 = st[2];
+  p.vec_scores =
+      aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && pr.N % 8 == 0;
+  return run_fwd(fn, p, pr, fas::kFwdScores, waves, stream);
 }
 
 int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum, const int64_t st[3],
                                void* stream) {
   static const char* fn = "fas_attention_with_row_sum";
-  fas::KParams p;
+  Problem pr;
   int rc;
-  if ((rc = fill_common(fn, a, &p, false))) return rc;
-  if (empty_launch(p)) return FAS_OK;
-  if ((rc = set_aux(fn, &p, row_sum, st, "row_sum"))) return rc;
-  // Every row is written by the kernel; no zero-fill needed.
-  return hip_status(fn, fas::launch_row_sum(p, a->dtype, (int)a->head_dim,
-                                            static_cast<hipStream_t>(stream)));
+  if ((rc = check_args(fn, a, &pr))) return rc;
+  if ((int64_t)pr.B * pr.H * pr.M == 0) return FAS_OK;
+  if ((rc = check_out3(fn, "row_sum", row_sum, st))) return rc;
+  const int waves = fwd_waves();
+  fas::FwdParams p = fwd_params(a, pr, false, fas::fwd_rows_per_block(pr.D, waves));
+  p.aux = row_sum;
+  p.sa0 = st[0];
+  p.sa1 = st[1];
+  p.sa2 = st[2];
+  return run_fwd(fn, p, pr, fas::kFwdRowSum, waves, stream);
 }
 
 int fas_attention_with_col_sum(const fas_attn_args* a, float* col_sum, const int64_t st[3],
-                               void* stream) {
-  static const char* fn = "fas_attention_with_col_sum";
-  fas::KParams p;
-  int rc;
-  if ((rc = fill_common(fn, a, &p, false))) return rc;
-  p.order = a->causal ? fas::kOrderReverse : fas::kOrderRoundRobin;
-  return run_col(fn, a, col_sum, st, a->seqlen_k, &p, fas::launch_col_sum, stream);
+                               void* ws, size_t ws_bytes, void* stream) {
+  return run_raw("fas_attention_with_col_sum", FAS_VARIANT_COL_SUM, a, 0, col_sum, st, ws,
+                 ws_bytes, stream);
 }
 
 int fas_attention_with_col_sum_sequential(const fas_attn_args* a, float* col_sum,
-                                          const int64_t st[3], void* stream) {
-  static const char* fn = "fas_attention_with_col_sum_sequential";
-  fas::KParams p;
-  int rc;
-  if ((rc = fill_common(fn, a, &p, false))) return rc;
-  p.order = fas::kOrderRoundRobin;
-  return run_col(fn, a, col_sum, st, a->seqlen_k, &p, fas::launch_col_sum, stream);
+                                          const int64_t st[3], void* ws, size_t ws_bytes,
+                                          void* stream) {
+  return run_raw("fas_attention_with_col_sum_sequential", FAS_VARIANT_COL_SUM_SEQUENTIAL, a, 0,
+                 col_sum, st, ws, ws_bytes, stream);
 }
 
 int fas_attention_with_softmax_col_sum(const fas_attn_args* a, float* col_sum, const int64_t st[3],
-                                       void* stream) {
-  static const char* fn = "fas_attention_with_softmax_col_sum";
-  fas::KParams p;
-  int rc;
-  if ((rc = fill_common(fn, a, &p, false))) return rc;
-  p.order = fas::kOrderRoundRobin;
-  p.order2 = a->causal ? fas::kOrderReverse : fas::kOrderRoundRobin;
-  return run_col(fn, a, col_sum, st, a->seqlen_k, &p, fas::launch_col_softmax, stream);
+                                       void* ws, size_t ws_bytes, void* stream) {
+  return run_softmax("fas_attention_with_softmax_col_sum", FAS_VARIANT_SOFTMAX_COL_SUM, a, 0,
+                     col_sum, st, ws, ws_bytes, stream);
 }
 
 int fas_attention_cross_token_qk_sum(const fas_attn_args* a, int64_t split, float* cross,
-                                     const int64_t st[3], void* stream) {
-  static const char* fn = "fas_attention_cross_token_qk_sum";
-  fas::KParams p;
-  int rc;
-  if ((rc = fill_common(fn, a, &p, true))) return rc;
-  if ((rc = check_split(fn, a, split))) return rc;
-  p.split = (int)split;
-  return run_col(fn, a, cross, st, split, &p, fas::launch_cross_qk, stream);
+                                     const int64_t st[3], void* ws, size_t ws_bytes, void* stream) {
+  return run_raw("fas_attention_cross_token_qk_sum", FAS_VARIANT_CROSS_QK_SUM, a, split, cross, st,
+                 ws, ws_bytes, stream);
 }
 
 int fas_attention_cross_token_softmax_sum(const fas_attn_args* a, int64_t split, float* cross,
-                                          const int64_t st[3], void* stream) {
-  static const char* fn = "fas_attention_cross_token_softmax_sum";
-  fas::KParams p;
-  int rc;
-  if ((rc = fill_common(fn, a, &p, false))) return rc;
-  if ((rc = check_split(fn, a, split))) return rc;
-  p.split = (int)split;
-  p.order = fas::kOrderRoundRobin;
-  return run_col(fn, a, cross, st, split, &p, fas::launch_cross_softmax, stream);
-}
-
-size_t fas_cross_token_softmax_sum_buffered_workspace_bytes(const fas_attn_args* a, int64_t split) {
-  if (a == nullptr || split <= 0) return 0;
-  const int64_t rows = a->seqlen_q > split ? a->seqlen_q - split : 0;
-  return (size_t)(a->batch * a->heads_q * rows * split) * sizeof(float);
+                                          const int64_t st[3], void* ws, size_t ws_bytes,
+                                          void* stream) {
+  return run_softmax("fas_attention_cross_token_softmax_sum", FAS_VARIANT_CROSS_SOFTMAX_SUM, a,
+                     split, cross, st, ws, ws_bytes, stream);
 }
 
 int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64_t split,
-                                                   float* cross, const int64_t st[3],
-                                                   void* workspace, size_t workspace_bytes,
-                                                   void* stream) {
-  static const char* fn = "fas_attention_cross_token_softmax_sum_buffered";
-  fas::KParams p;
-  int rc;
-  if ((rc = fill_common(fn, a, &p, false))) return rc;
-  if ((rc = check_split(fn, a, split))) return rc;
-  p.split = (int)split;
-  const size_t need = fas_cross_token_softmax_sum_buffered_workspace_bytes(a, split);
-  if (need > 0) {
-    if (workspace == nullptr || workspace_bytes < need)
-      return fail(FAS_ERR_WORKSPACE, fn, "workspace of %zu bytes needed, %zu given", need,
-                  workspace_bytes);
-    if (!aligned16(workspace)) return fail(FAS_ERR_INVALID, fn, "workspace not 16-byte aligned");
-  }
-  const int64_t rows = a->seqlen_q > split ? a->seqlen_q - split : 0;
-  p.buf = static_cast<float*>(workspace);
-  p.sb2 = split;
-  p.sb1 = rows * split;
-  p.sb0 = a->heads_q * rows * split;
-  return run_col(fn, a, cross, st, split, &p, fas::launch_cross_softmax_buf, stream);
+                                                   float* cross, const int64_t st[3], void* ws,
+                                                   size_t ws_bytes, void* stream) {
+  return run_softmax("fas_attention_cross_token_softmax_sum_buffered",
+                     FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED, a, split, cross, st, ws, ws_bytes,
+                     stream);
 }
 
 }  // extern "C"

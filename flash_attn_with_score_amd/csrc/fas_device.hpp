@@ -1,0 +1,152 @@
+// Device-side building blocks shared by the gfx950 kernels: element traits
+// (fp16 / bf16 MFMA and packing), buffer descriptors, the LDS tile layout and
+// the MFMA operand fetches from it.
+//
+// MFMA used throughout: v_mfma_f32_32x32x16_{f16,bf16}.  Operand layout for
+// lane l (c = l % 32, g = l / 32): A supplies row c, contraction indices
+// 8g..8g+7; B supplies column c, the same contraction indices; the 32x32
+// fp32 accumulator gives lane l column c and rows 8*(r/4) + 4g + r%4 for
+// register r = 0..15.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fas {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __fp16 fp16x4_lds __attribute__((__vector_size__(4 * sizeof(__fp16))));
+
+#define FAS_LDS __attribute__((address_space(3)))
+
+// Buffer descriptor word 3 for gfx9-family raw buffers.
+constexpr int kRsrcWord3 = 0x00020000;
+// Buffer access flags: nontemporal (streaming) stores.
+constexpr int kAuxNT = 2;
+
+struct F16 {
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // Round-to-nearest-even conversion of two floats packed lo | hi << 16.
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, f16x2));
+  }
+  static __device__ __forceinline__ uint16_t cvt(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return (float)__builtin_bit_cast(_Float16, x);
+  }
+};
+
+struct BF16 {
+  static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));
+  }
+  static __device__ __forceinline__ uint16_t cvt(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return __builtin_bit_cast(float, (uint32_t)x << 16);
+  }
+};
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
+__device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
+__device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float log2f_fast(float x) { return __builtin_amdgcn_logf(x); }
+
+// Raw buffer over [base, base + bytes): loads past the end return 0, stores
+// past the end are dropped.  Offsets are 32-bit byte offsets.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store16(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_store16_nt(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kAuxNT);
+}
+
+// Row permutation applied to MFMA operand rows (bits 2 and 3 swapped).  With
+// it the 16 accumulator registers of lane l (g = l / 32) cover rows
+// {16*(r/8) + 8g + r%8}: two runs of 8 consecutive rows, so a lane's values
+// can leave as 16-byte vectors.
+__device__ __forceinline__ int perm_row(int c) {
+  return (c & 0x13) | ((c & 4) << 1) | ((c & 8) >> 1);
+}
+// Row index (within a 32-row block) of accumulator register r of lane group g.
+__device__ __forceinline__ int acc_row(int r, int g) { return 16 * (r >> 3) + 8 * g + (r & 7); }
+
+// LDS tile of 16-bit elements, `rows` x D, row-major with the 16-byte chunks
+// of each row XOR-permuted by swz(row).  The permutation keeps both operand
+// fetches below free of bank conflicts: 16 lanes reading one logical chunk
+// from 16 consecutive rows (ds_read_b128), and 32 lanes reading 4 rows x 64
+// bytes with the transposing ds_read_b64_tr_b16.
+template <int D>
+__device__ __forceinline__ int swz(int row) {
+  if constexpr (D == 128) {
+    return ((row & 3) << 2) | ((row >> 2) & 3);
+  } else if constexpr (D == 64) {
+    const int t = (row >> 1) & 7;
+    return ((t & 1) << 2) | ((t >> 1) & 3);
+  } else if constexpr (D == 32) {
+    return (row >> 2) & 3;
+  } else {
+    return (row >> 3) & 1;
+  }
+}
+// Element offset of (row, logical 16-byte chunk ch) in a swizzled tile.
+template <int D>
+__device__ __forceinline__ int tile_off(int row, int ch) {
+  return row * D + ((ch ^ swz<D>(row)) << 3);
+}
+
+// A/B operand fetch for a contraction over the head dim: lane (c, g) gets
+// elements [16*ks + 8g, +8) of tile row `row`.
+template <int D>
+__device__ __forceinline__ u32x4 lds_row_chunk(const uint16_t* tile, int row, int ks, int g) {
+  return *reinterpret_cast<const u32x4*>(tile + tile_off<D>(row, 2 * ks + g));
+}
+
+// Transposing fetch of the A operand V^T for O^T += V^T P^T: rows of the
+// MFMA are head dims (block db: dims 32db + perm_row(c)), contraction index
+// 8g + e is key 16*cs + 8g + e of the tile.  ds_read_b64_tr_b16 hands lane i
+// of each 16-lane group element i%4 of the 8-byte rows fetched by lanes
+// i/4 + 4e; the fetch addresses below make that the column of 4 keys of one
+// head dim.
+template <int D>
+__device__ __forceinline__ u32x4 lds_vt_operand(const uint16_t* vtile, int db, int cs, int lane) {
+  const int g = lane >> 5, half = (lane >> 4) & 1, j = lane & 15;
+  const int jj = j & 3;
+  const int sw = ((jj & 1) << 1) | (jj >> 1);  // swap the two bits of j % 4
+  int dim = 32 * db + 16 * half + 4 * sw;
+  if constexpr (D < 32) dim &= D - 1;  // rows past the head dim duplicate (never stored)
+  const int key = 16 * cs + 8 * g + (j >> 2);
+  const int ch = dim >> 3, sub = dim & 7;
+  const uint16_t* p0 = vtile + tile_off<D>(key, ch) + sub;
+  const uint16_t* p1 = vtile + tile_off<D>(key + 4, ch) + sub;
+  const fp16x4_lds r0 = __builtin_amdgcn_ds_read_tr16_b64_v4f16((FAS_LDS fp16x4_lds*)(p0));
+  const fp16x4_lds r1 = __builtin_amdgcn_ds_read_tr16_b64_v4f16((FAS_LDS fp16x4_lds*)(p1));
+  const u32x2 a = __builtin_bit_cast(u32x2, r0), b = __builtin_bit_cast(u32x2, r1);
+  return u32x4{a.x, a.y, b.x, b.y};
+}
+
+}  // namespace fas

@@ -1,7 +1,7 @@
-// Zero-fill of the fp32 sum accumulators.  A kernel rather than
-// hipMemsetAsync: memset nodes have misbehaved under HIP graph replay on this
-// platform, and the sum outputs may be strided views.
-#include "fas_kernel.hpp"
+// Zero-fill of strided fp32 outputs for degenerate shapes (no query rows or
+// no keys).  A kernel rather than hipMemsetAsync so a captured launch
+// sequence holds no memset node, and because the outputs may be strided.
+#include "fas_launch.hpp"
 
 namespace fas {
 
@@ -23,9 +23,9 @@ hipError_t launch_fill_zero(float* p, int64_t s0, int64_t s1, int64_t s2, int64_
   if (total <= 0) return hipSuccess;
   int64_t blocks = (total + 255) / 256;
   if (blocks > 4096) blocks = 4096;
-  void* args[] = {&p, &s0, &s1, &s2, &n0, &n1, &n2};
-  return hipLaunchKernel(reinterpret_cast<const void*>(&fill_zero_3d), dim3((unsigned)blocks),
-                         dim3(256), args, 0, s);
+  hipLaunchKernelGGL(fill_zero_3d, dim3((unsigned)blocks), dim3(256), 0, s, p, s0, s1, s2, n0, n1,
+                     n2);
+  return hipGetLastError();
 }
 
 }  // namespace fas

@@ -1,6 +1,5 @@
-// Host-side launchers of the gfx950 kernels, one per side-product mode.
-// Each is defined in its own translation unit (fas_mode_*.hip) so the
-// template instantiations compile in parallel.
+// Host-side launchers of the gfx950 kernels.  Each family is instantiated in
+// its own translation unit so the template instances compile in parallel.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -9,14 +8,19 @@
 
 namespace fas {
 
-// One launcher per mode, each instantiated in its own translation unit.
-hipError_t launch_scores(const KParams& p, int dtype, int d, hipStream_t s);
-hipError_t launch_row_sum(const KParams& p, int dtype, int d, hipStream_t s);
-hipError_t launch_col_sum(const KParams& p, int dtype, int d, hipStream_t s);
-hipError_t launch_cross_qk(const KParams& p, int dtype, int d, hipStream_t s);
-hipError_t launch_col_softmax(const KParams& p, int dtype, int d, hipStream_t s);
-hipError_t launch_cross_softmax(const KParams& p, int dtype, int d, hipStream_t s);
-hipError_t launch_cross_softmax_buf(const KParams& p, int dtype, int d, hipStream_t s);
+// Forward pass (fas_fwd.hpp); mode is a FwdMode, dtype 0 = fp16, 1 = bf16.
+// waves selects 4 or 8 wave64s per workgroup (head dim 128 only).
+hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, int waves, hipStream_t s);
+// Rows per workgroup of launch_fwd for (d, waves).
+int fwd_rows_per_block(int d, int waves);
+
+// Softmax-weight column sums after a forward pass that wrote lse2.
+hipError_t launch_colsm(const ColsmParams& p, int dtype, int d, bool buffered, hipStream_t s);
+hipError_t launch_group_reduce(const float* part, float* out, int64_t so0, int64_t so1,
+                               int64_t so2, int B, int Hk, int G, int ncols, hipStream_t s);
+// Raw-score column sums: block sums of q, suffix scan, per-key dot products.
+hipError_t launch_rawsum(const RawParams& p, int dtype, bool suffix, hipStream_t s);
+
 hipError_t launch_fill_zero(float* p, int64_t s0, int64_t s1, int64_t s2, int64_t n0, int64_t n1,
                             int64_t n2, hipStream_t s);
 

@@ -1,54 +1,86 @@
-// Kernel-side parameter block shared by the host dispatcher (fas_api.cpp)
-// and the gfx950 kernels (fas_kernel.hpp).  Plain data only.
+// Kernel-side parameter blocks shared by the host dispatcher (fas_api.cpp)
+// and the gfx950 kernels (fas_fwd.hpp, fas_sums.hpp).  Plain data only.
 #pragma once
 #include <stdint.h>
 
 namespace fas {
 
-// Query rows per workgroup; the host sizes the grid with it.
-constexpr int kBMHost = 128;
-
-// Side product a launch computes besides the attention output.
-enum Mode : int {
-  kModeScores = 0,         // full (B,Hq,M,N) score matrix, masked -> 0
-  kModeRowSum = 1,         // (B,Hq,M) sum of scaled raw scores
-  kModeColSum = 2,         // (B,Hk,N) sum of scaled raw scores
-  kModeCrossQk = 3,        // (B,Hk,split) raw sum, rows >= split, keys < split
-  kModeColSoftmax = 4,     // (B,Hk,N) sum of final softmax weights (2 passes)
-  kModeCrossSoftmax = 5,   // (B,Hk,split) softmax-weight sum (2 passes)
-  kModeCrossSoftmaxBuf = 6 // as 5, pass 2 reloads fp32 scores from scratch
+// Side product of the forward kernel (fas_fwd.hpp).
+enum FwdMode : int {
+  kFwdPlain = 0,   // output (+ optional base-2 LSE)
+  kFwdScores = 1,  // + (B,H,M,N) scaled scores, masked -> 0
+  kFwdRowSum = 2,  // + (B,H,M) row sums of scaled scores
+  kFwdRegion = 3   // + fp32 raw scores of rows >= split, keys < split
 };
 
-// Order in which a workgroup visits its key tiles.  Only the fp32 summation
-// order of the side products depends on it.
-enum Order : int { kOrderForward = 0, kOrderReverse = 1, kOrderRoundRobin = 2 };
-
-struct KParams {
+struct FwdParams {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* v;
   uint16_t* o;
-  float* lse;        // optional
-  uint16_t* scores;  // kModeScores
-  float* aux;        // row / column / cross sums
-  float* buf;        // kModeCrossSoftmaxBuf scratch
+  float* lse2;       // optional (B*H, M) contiguous: m*qk_scale + log2(l), +inf for empty rows
+  uint16_t* scores;  // kFwdScores
+  float* aux;        // kFwdRowSum: (B,H,M) strided
+  float* region;     // kFwdRegion: (B*H, M - split, split) contiguous fp32
   int64_t sq0, sq1, sq2;
   int64_t sk0, sk1, sk2;
   int64_t sv0, sv1, sv2;
   int64_t so0, so1, so2;
-  int64_t ss0, ss1, ss2;  // scores
-  int64_t sa0, sa1, sa2;  // aux
-  int64_t sl0, sl1, sl2;  // lse
-  int64_t sb0, sb1, sb2;  // buf: (B, Hq, M - split, split)
+  int64_t ss0, ss1, ss2;
+  int64_t sa0, sa1, sa2;
+  uint32_t q_bytes, k_bytes, v_bytes, o_bytes;  // per-(b, head) buffer extents
+  uint32_t qneg;     // 0x80008000 to negate q (negative sm_scale), else 0
   int B, H, G, M, N, split;
-  int causal;      // 0/1
-  int causal_off;  // key j admissible for query i iff causal_off + i >= j
-  int order;       // pass-1 tile order (Order)
-  int order2;      // pass-2 tile order (Order)
-  int nrb;         // number of 128-row query blocks
-  int vec_scores;  // 1 when every score row start is 16-byte aligned
-  float sm_scale;
-  float qk_scale;  // sm_scale * log2(e)
+  int causal;
+  int causal_off;    // key j admissible for query i iff causal_off + i >= j
+  int nrb;           // query row blocks
+  int vec_scores;    // scores rows 16-byte aligned and N % 8 == 0
+  int vec_region;    // split % 4 == 0
+  float sm_scale;    // |sm_scale|
+  float qk_scale;    // |sm_scale| * log2(e)
+};
+
+}  // namespace fas
+
+namespace fas {
+
+// Key-outer column sums of the softmax weights (fas_sums.hpp).
+struct ColsmParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const float* lse2;     // (B*H, M) base-2 LSE from the forward pass
+  const float* region;   // buffered source: (B*H, M - split, split) raw fp32 scores
+  float* out;            // G == 1: (B, Hk, ncols) strided output; else partials (B*H, ncols)
+  int64_t sq0, sq1, sq2;
+  int64_t sk0, sk1, sk2;
+  int64_t so0, so1, so2;  // output strides (G == 1) or (H*ncols, ncols, 1)
+  uint32_t q_bytes, k_bytes;
+  uint32_t qneg;
+  int B, H, G, M, N;
+  int row_lo;            // first query row that contributes (0, or split)
+  int ncols;             // keys summed: N, or split
+  int split;             // region row offset / pitch (buffered)
+  int causal, causal_off;
+  int nkb;               // key blocks
+  float qk_scale;        // |sm_scale| * log2(e)
+};
+
+// Raw-score column sums by linearity: sum_i (q_i . k_j) = (sum_i q_i) . k_j.
+struct RawParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  float* bsum;           // (B*Hk, nblk + 1, D) fp32 block sums -> exclusive suffix sums
+  float* out;            // (B, Hk, ncols) strided
+  int64_t sq0, sq1, sq2;
+  int64_t sk0, sk1, sk2;
+  int64_t so0, so1, so2;
+  int B, H, G, Hk, M, N, D;
+  int row_lo;            // rows [row_lo, M) contribute
+  int nblk;              // 64-row blocks of [row_lo, M)
+  int ncols;
+  int causal, causal_off;
+  int nextra;            // causal: key blocks below causal_off (all rows admissible)
+  float sm_scale;        // signed
 };
 
 }  // namespace fas

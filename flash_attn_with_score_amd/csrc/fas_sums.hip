@@ -1,0 +1,84 @@
+// Instances and launchers of the column-sum kernels (fas_sums.hpp).
+#include "fas_launch.hpp"
+#include "fas_sums.hpp"
+
+namespace fas {
+
+template <class E, int D>
+static hipError_t colsm_t(const ColsmParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)p.nkb * p.B * p.H));
+  hipLaunchKernelGGL((colsm_kernel<E, D>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_colsm(const ColsmParams& p, int dtype, int d, bool buffered, hipStream_t s) {
+  if (buffered) {
+    const dim3 grid((unsigned)((int64_t)p.nkb * p.B * p.H));
+    hipLaunchKernelGGL(colsm_buffered_kernel, grid, dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
+  if (dtype == 0) {
+    switch (d) {
+      case 16: return colsm_t<F16, 16>(p, s);
+      case 32: return colsm_t<F16, 32>(p, s);
+      case 64: return colsm_t<F16, 64>(p, s);
+      case 128: return colsm_t<F16, 128>(p, s);
+    }
+  } else {
+    switch (d) {
+      case 16: return colsm_t<BF16, 16>(p, s);
+      case 32: return colsm_t<BF16, 32>(p, s);
+      case 64: return colsm_t<BF16, 64>(p, s);
+      case 128: return colsm_t<BF16, 128>(p, s);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_group_reduce(const float* part, float* out, int64_t so0, int64_t so1,
+                               int64_t so2, int B, int Hk, int G, int ncols, hipStream_t s) {
+  const int64_t total = (int64_t)B * Hk * ncols;
+  if (total <= 0) return hipSuccess;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(group_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, part, out, so0,
+                     so1, so2, B, Hk, G, ncols);
+  return hipGetLastError();
+}
+
+template <class E, int D>
+static hipError_t rawsum_t(const RawParams& p, bool suffix, hipStream_t s) {
+  const unsigned bhk = (unsigned)(p.B * p.Hk);
+  if (p.nblk > 0)
+    hipLaunchKernelGGL((qsum_blocks_kernel<E, D>), dim3((unsigned)p.nblk, bhk), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(suffix_blocks_kernel, dim3(bhk), dim3(D < 64 ? 64 : D), 0, s, p);
+  if (suffix) {
+    const unsigned nw = (unsigned)((p.M + 63) / 64 + p.nextra);
+    if (nw > 0) hipLaunchKernelGGL((colraw_kernel<E, D, true>), dim3(nw, bhk), dim3(256), 0, s, p);
+  } else {
+    const unsigned nw = (unsigned)((p.ncols + 63) / 64);
+    if (nw > 0) hipLaunchKernelGGL((colraw_kernel<E, D, false>), dim3(nw, bhk), dim3(256), 0, s, p);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_rawsum(const RawParams& p, int dtype, bool suffix, hipStream_t s) {
+  if (dtype == 0) {
+    switch (p.D) {
+      case 16: return rawsum_t<F16, 16>(p, suffix, s);
+      case 32: return rawsum_t<F16, 32>(p, suffix, s);
+      case 64: return rawsum_t<F16, 64>(p, suffix, s);
+      case 128: return rawsum_t<F16, 128>(p, suffix, s);
+    }
+  } else {
+    switch (p.D) {
+      case 16: return rawsum_t<BF16, 16>(p, suffix, s);
+      case 32: return rawsum_t<BF16, 32>(p, suffix, s);
+      case 64: return rawsum_t<BF16, 64>(p, suffix, s);
+      case 128: return rawsum_t<BF16, 128>(p, suffix, s);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fas

@@ -1,0 +1,368 @@
+// gfx950 kernels for the column-type side products.
+//
+// Softmax-weight column sums (attention_with_col_softmax_sum.py:195-270,
+// attention_cross_token_softmax_sum.py:203-268 and the buffered :568-627)
+// are computed after the forward pass, key-block outer: a workgroup owns 256
+// keys of one (batch, query head), keeps them in VGPRs and streams the query
+// rows that can see them.  S = Q K^T puts keys on lanes and queries in the
+// accumulator registers, so P = exp2(s*qk_scale - lse2[row]) (the forward
+// pass's final base-2 log-sum-exp) is summed over queries in-lane.  Every
+// column is owned by one workgroup: no atomics, the result is deterministic.
+// GQA groups are folded afterwards by group_reduce_kernel in a fixed order.
+//
+// Raw-score column sums (attention_with_col_sum.py:186-191,
+// attention_with_col_sum_sequential.py:177-182,
+// attention_cross_token_qk_sum.py:169-216) are linear in q:
+//   sum_{i admissible for j} (q_i . k_j) * sm_scale = (sum_i q_i) . k_j * sm_scale
+// so they need per-64-row block sums of q (qsum_blocks_kernel), their
+// exclusive suffix sums (suffix_blocks_kernel) and one dot product per key
+// (colraw_kernel): O(N*D) work and one read of Q and K instead of a
+// reduction over the N*N score matrix.
+#pragma once
+#include "fas_device.hpp"
+#include "fas_params.hpp"
+
+namespace fas {
+
+// ---------------------------------------------------------------- softmax
+
+__device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb, int& bh) {
+  // Same XCD-aware dealing as the forward kernel; key blocks ascending, which
+  // for causal masks is longest first.
+  if ((BH & 7) == 0) {
+    const int x = bid & 7, s = bid >> 3, per = BH >> 3;
+    bh = x * per + s % per;
+    kb = s / per;
+  } else {
+    bh = bid % BH;
+    kb = bid / BH;
+  }
+}
+
+template <class E, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void colsm_kernel(const ColsmParams p) {
+  constexpr int KS = D / 16;
+  constexpr int NT = 256;
+  constexpr int KW = 64;            // keys per wave
+  constexpr int BK = 4 * KW;        // keys per workgroup
+  constexpr int TQ = 64;            // query rows per tile
+  constexpr int CPR = D / 8;
+  constexpr int CHUNKS = TQ * CPR;
+  constexpr int CPT = (CHUNKS + NT - 1) / NT;
+
+  __shared__ __attribute__((aligned(16))) uint16_t qlds[2][TQ * D];
+  __shared__ __attribute__((aligned(16))) float llds[2][TQ];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  int kb, bh;
+  map_block_keys(blockIdx.x, p.nkb, p.B * p.H, kb, bh);
+  const int h = bh % p.H, b = bh / p.H, hk = h / p.G;
+  const int key0 = kb * BK + KW * wave;
+
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
+  const float* lse = p.lse2 + (int64_t)bh * p.M;
+
+  // K (B operand of S = Q K^T): lane holds K[key0 + 32*kblk + c][16ks + 8g, +8).
+  u32x4 kreg[2][KS];
+#pragma unroll
+  for (int kblk = 0; kblk < 2; ++kblk)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+      kreg[kblk][ks] =
+          buf_load16(rk, (uint32_t)(((key0 + 32 * kblk + c) * p.sk2 + 16 * ks + 8 * g) * 2));
+
+  // Query tiles that can see any key of the workgroup.
+  int rstart = p.row_lo;
+  if (p.causal) rstart = max(rstart, kb * BK - p.causal_off);
+  const int t0 = max(0, rstart) / TQ;
+  const int t1 = (p.M + TQ - 1) / TQ;
+
+  u32x4 qst[CPT];
+  float lst = 0.f;
+  auto fetch = [&](int t) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int id = tid + i * NT;
+      const int row = id / CPR, ch = id % CPR;
+      qst[i] = buf_load16(rq, (uint32_t)(((t * TQ + row) * p.sq2 + ch * 8) * 2)) ^ p.qneg;
+    }
+    if (tid < TQ) {
+      const int row = t * TQ + tid;
+      lst = (row < p.row_lo || row >= p.M) ? pos_inf() : lse[row];
+    }
+  };
+  auto stash = [&](int stage) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int id = tid + i * NT;
+      if (CHUNKS % NT == 0 || id < CHUNKS) {
+        const int row = id / CPR, ch = id % CPR;
+        *reinterpret_cast<u32x4*>(&qlds[stage][tile_off<D>(row, ch)]) = qst[i];
+      }
+    }
+    if (tid < TQ) llds[stage][tid] = lst;
+  };
+
+  float colacc[2] = {0.f, 0.f};
+  if (t0 < t1) {
+    fetch(t0);
+    stash(0);
+  }
+  __syncthreads();
+  for (int t = t0; t < t1; ++t) {
+    const int stage = (t - t0) & 1;
+    const bool more = t + 1 < t1;
+    if (more) fetch(t + 1);
+    const int r0 = t * TQ;
+    bool live = true, full = true;
+    if (p.causal) {
+      live = p.causal_off + r0 + TQ - 1 >= key0;
+      full = p.causal_off + r0 >= key0 + KW - 1;
+    }
+    if (live) {
+      const uint16_t* qt = qlds[stage];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const u32x4 a = lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g);
+          s[0] = E::mma(a, kreg[0][ks], s[0]);
+          s[1] = E::mma(a, kreg[1][ks], s[1]);
+        }
+        // Register r holds query row r0 + 32qb + acc_row(r, g).
+        float lr[16];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const float* lp = &llds[stage][32 * qb + 16 * hf + 8 * g];
+          const f32x4 x0 = *reinterpret_cast<const f32x4*>(lp);
+          const f32x4 x1 = *reinterpret_cast<const f32x4*>(lp + 4);
+          lr[8 * hf + 0] = x0.x; lr[8 * hf + 1] = x0.y; lr[8 * hf + 2] = x0.z; lr[8 * hf + 3] = x0.w;
+          lr[8 * hf + 4] = x1.x; lr[8 * hf + 5] = x1.y; lr[8 * hf + 6] = x1.z; lr[8 * hf + 7] = x1.w;
+        }
+#pragma unroll
+        for (int kblk = 0; kblk < 2; ++kblk) {
+          const int key = key0 + 32 * kblk + c;
+          float acc = 0.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float pr = exp2f_fast(fmaf(s[kblk][r], p.qk_scale, -lr[r]));
+            if (!full) {
+              const int row = r0 + 32 * qb + acc_row(r, g);
+              if (p.causal_off + row < key) pr = 0.f;
+            }
+            acc += pr;
+          }
+          colacc[kblk] += acc;
+        }
+      }
+    }
+    if (more) stash(stage ^ 1);
+    __syncthreads();
+  }
+#pragma unroll
+  for (int kblk = 0; kblk < 2; ++kblk) {
+    const float tot = colacc[kblk] + __shfl_xor(colacc[kblk], 32);
+    const int key = key0 + 32 * kblk + c;
+    if (g == 0 && key < p.ncols) p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot;
+  }
+}
+
+// Buffered source: pass 1 left the raw fp32 scores of the region
+// (rows >= split, keys < split) in p.region; each thread owns one key and
+// walks the rows, so every row read is 1 KiB contiguous per workgroup.
+__global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p) {
+  int kb, bh;
+  map_block_keys(blockIdx.x, p.nkb, p.B * p.H, kb, bh);
+  const int h = bh % p.H, b = bh / p.H;
+  const int key = kb * 256 + threadIdx.x;
+  const int rows = max(0, p.M - p.split);
+  if (key >= p.ncols) return;
+  const float* reg = p.region + (int64_t)bh * rows * p.split + key;
+  const float* lse = p.lse2 + (int64_t)bh * p.M;
+  int rstart = p.split;
+  if (p.causal) rstart = max(rstart, key - p.causal_off);
+  float acc = 0.f;
+  int row = rstart;
+  for (; row + 4 <= p.M; row += 4) {
+    float s[4], l[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      s[u] = reg[(int64_t)(row + u - p.split) * p.split];
+      l[u] = lse[row + u];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += exp2f_fast(fmaf(s[u], p.qk_scale, -l[u]));
+  }
+  for (; row < p.M; ++row)
+    acc += exp2f_fast(fmaf(reg[(int64_t)(row - p.split) * p.split], p.qk_scale, -lse[row]));
+  p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = acc;
+}
+
+// out[b, hk, j] = sum over the G query heads of group hk of part[b*H + h, j],
+// heads added in increasing order.
+__global__ void group_reduce_kernel(const float* __restrict__ part, float* out, int64_t so0,
+                                    int64_t so1, int64_t so2, int B, int Hk, int G, int ncols) {
+  const int64_t total = (int64_t)B * Hk * ncols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int j = (int)(i % ncols);
+    const int64_t bhk = i / ncols;
+    const int hk = (int)(bhk % Hk), b = (int)(bhk / Hk);
+    const float* src = part + ((int64_t)b * Hk * G + (int64_t)hk * G) * ncols + j;
+    float acc = 0.f;
+    for (int gg = 0; gg < G; ++gg) acc += src[(int64_t)gg * ncols];
+    out[b * so0 + hk * so1 + (int64_t)j * so2] = acc;
+  }
+}
+
+// ---------------------------------------------------------------- raw sums
+
+template <class E>
+__device__ __forceinline__ void unpack8(u32x4 v, float (&x)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    x[2 * w] = E::to_f32((uint16_t)(v[w] & 0xffffu));
+    x[2 * w + 1] = E::to_f32((uint16_t)(v[w] >> 16));
+  }
+}
+
+// bsum[bhk][blk][:] = sum over the group's query heads and the rows
+// [row_lo + 64*blk, +64) of q (fp32).
+template <class E, int D>
+__global__ __launch_bounds__(256) void qsum_blocks_kernel(const RawParams p) {
+  constexpr int CPR = D / 8;          // threads per row
+  constexpr int RPI = 256 / CPR;      // rows in flight
+  __shared__ float red[RPI][D];
+  const int blk = blockIdx.x, bhk = blockIdx.y;
+  const int hk = bhk % p.Hk, b = bhk / p.Hk;
+  const int ch = threadIdx.x % CPR, rg = threadIdx.x / CPR;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int r0 = p.row_lo + 64 * blk;
+  const int r1 = min(p.M, r0 + 64);
+  for (int gg = 0; gg < p.G; ++gg) {
+    const uint16_t* qh = p.q + b * p.sq0 + (int64_t)(hk * p.G + gg) * p.sq1 + ch * 8;
+    for (int row = r0 + rg; row < r1; row += RPI) {
+      float x[8];
+      unpack8<E>(*reinterpret_cast<const u32x4*>(qh + (int64_t)row * p.sq2), x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += x[e];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) red[rg][ch * 8 + e] = acc[e];
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float s = 0.f;
+    for (int r = 0; r < RPI; ++r) s += red[r][d];
+    p.bsum[((int64_t)bhk * (p.nblk + 1) + blk) * D + d] = s;
+  }
+}
+
+// In place: bsum[blk] <- sum of blocks after blk; bsum[nblk] <- total.
+__global__ void suffix_blocks_kernel(const RawParams p) {
+  const int bhk = blockIdx.x;
+  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+    float* col = p.bsum + (int64_t)bhk * (p.nblk + 1) * p.D + d;
+    float acc = 0.f;
+    for (int blk = p.nblk - 1; blk >= 0; --blk) {
+      const float t = col[(int64_t)blk * p.D];
+      col[(int64_t)blk * p.D] = acc;
+      acc += t;
+    }
+    col[(int64_t)p.nblk * p.D] = acc;
+  }
+}
+
+// One dot product per key with a per-key fp32 vector held in LDS rows.
+template <class E, int D>
+__device__ __forceinline__ float key_dot(const RawParams& p, const uint16_t* kbase, int key,
+                                         const float* vec, int part) {
+  constexpr int DP = D / 4;  // dims per thread (4 threads per key)
+  const uint16_t* kr = kbase + (int64_t)key * p.sk2 + part * DP;
+  float acc = 0.f;
+#pragma unroll
+  for (int d8 = 0; d8 < DP; d8 += 8) {
+    float x[8];
+    if constexpr (DP >= 8) {
+      unpack8<E>(*reinterpret_cast<const u32x4*>(kr + d8), x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = e < DP ? E::to_f32(kr[d8 + e]) : 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (d8 + e < DP) acc = fmaf(x[e], vec[part * DP + d8 + e], acc);
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  return acc;
+}
+
+// Causal column sums: workgroup w < nextra handles keys [64w, 64w+64) below
+// causal_off (every row admissible); the others own one 64-row block rb and
+// the keys j = row + causal_off of its rows.  Non-causal / cross: every
+// workgroup owns 64 keys and uses the total.
+template <class E, int D, bool SUFFIX>
+__global__ __launch_bounds__(256) void colraw_kernel(const RawParams p) {
+  __shared__ float vec[64][D];
+  const int bhk = blockIdx.y;
+  const int hk = bhk % p.Hk, b = bhk / p.Hk;
+  const float* bs = p.bsum + (int64_t)bhk * (p.nblk + 1) * D;
+  const uint16_t* kbase = p.k + b * p.sk0 + hk * p.sk1;
+  const int w = blockIdx.x;
+  const int kslot = threadIdx.x >> 2, part = threadIdx.x & 3;
+
+  if (!SUFFIX || w < p.nextra) {
+    for (int d = threadIdx.x; d < D; d += 256) vec[0][d] = bs[(int64_t)p.nblk * D + d];
+    __syncthreads();
+    const int key = 64 * w + kslot;
+    const int lim = SUFFIX ? min(p.ncols, p.causal_off) : p.ncols;
+    if (key < lim) {
+      const float dot = key_dot<E, D>(p, kbase, key, vec[0], part);
+      if (part == 0) p.out[b * p.so0 + hk * p.so1 + (int64_t)key * p.so2] = dot * p.sm_scale;
+    }
+    return;
+  }
+  // In-block suffix sums over rows [64rb, 64rb + 64) of the group's heads.
+  const int rb = w - p.nextra;
+  const int r0 = 64 * rb;
+  for (int i = threadIdx.x; i < 64 * D; i += 256) (&vec[0][0])[i] = 0.f;
+  __syncthreads();
+  {
+    constexpr int CPR = D / 8;
+    constexpr int RPI = 256 / CPR;
+    const int ch = threadIdx.x % CPR, rg = threadIdx.x / CPR;
+    for (int gg = 0; gg < p.G; ++gg) {
+      const uint16_t* qh = p.q + b * p.sq0 + (int64_t)(hk * p.G + gg) * p.sq1 + ch * 8;
+      for (int rr = rg; rr < 64; rr += RPI) {
+        const int row = r0 + rr;
+        if (row >= p.M) break;
+        float x[8];
+        unpack8<E>(*reinterpret_cast<const u32x4*>(qh + (int64_t)row * p.sq2), x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vec[rr][ch * 8 + e] += x[e];
+      }
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += 256) {
+    float acc = bs[(int64_t)rb * D + d];
+    for (int rr = 63; rr >= 0; --rr) {
+      acc += vec[rr][d];
+      vec[rr][d] = acc;
+    }
+  }
+  __syncthreads();
+  const int row = r0 + kslot;
+  const int key = row + p.causal_off;
+  if (row < p.M && key >= 0 && key < p.ncols) {
+    const float dot = key_dot<E, D>(p, kbase, key, vec[kslot], part);
+    if (part == 0) p.out[b * p.so0 + hk * p.so1 + (int64_t)key * p.so2] = dot * p.sm_scale;
+  }
+}
+
+}  // namespace fas

@@ -2,34 +2,38 @@
  * fas.h -- C ABI of the MI355X (gfx950) fused flash-attention-forward family
  * ("flash attention with scores").
  *
- * One entry point per reference launcher.  Each takes the shared attention
- * description (fas_attn_args: q/k/v/out device pointers, element strides,
- * sizes, dtype, causal flag, softmax scale) plus the side output of that
- * variant, and enqueues the work asynchronously on the given HIP stream.
- * Nothing here allocates device memory: every output, and the scratch buffer
- * of the buffered cross-token variant, is owned by the caller.
+ * One entry point per launcher of the reference package.  Each takes the
+ * shared attention description (fas_attn_args: q/k/v/out device pointers,
+ * element strides, sizes, dtype, causal flag, softmax scale) plus the side
+ * output of that variant, and enqueues its kernels asynchronously, in order,
+ * on the given HIP stream.  Nothing here allocates or frees device memory:
+ * every output and every workspace is owned by the caller, and no call
+ * synchronises with the host.
  *
  * Conventions shared by every entry point (they restate the reference's
  * Triton launchers; citations are to the reference checkout):
  *   - q is (B, Hq, M, D); k and v are (B, Hk, N, D); out is like q.  Only the
  *     innermost stride must be 1 (flash.py:23-26, maybe_contiguous); rows
- *     must be 16-byte aligned (pointer and strides[0..2] multiples of 8).
+ *     must be 16-byte aligned (pointer and strides[0..2] multiples of 8),
+ *     and one (batch, head) slice of any tensor must span < 2^31 bytes.
  *   - D in {16, 32, 64, 128}, Hq % Hk == 0; query head h reads KV head
  *     h / (Hq/Hk) (attention_with_scores.py:57).
  *   - Causal masking keeps (i, j) iff (N - M) + i >= j (bottom-right
  *     aligned, attention_with_scores.py:136) except in the cross-token
  *     QK-sum, which keeps i >= j (attention_cross_token_qk_sum.py:138).
- *   - Softmax state is fp32, computed in base 2 on raw scores with
+ *   - Softmax is computed in base 2 on raw scores with
  *     qk_scale = sm_scale * log2(e) (attention_with_scores.py:53-54,165-183).
  *   - Query rows with no admissible key (causal, M > N) produce out = 0 and
- *     a zero row sum (attention_with_scores.py:192-195).
+ *     zero sums (attention_with_scores.py:192-195).
  *   - Column-type sums are per KV head: the Hq/Hk query heads of a group are
  *     folded into one (B, Hk, *) vector (attention_with_col_sum.py:72,370).
- *   - Sum outputs are fp32 and are zeroed by the entry point itself before
- *     accumulation (the reference zero-fills with torch.zeros).
+ *   - Every element of every output is written by the call; outputs need no
+ *     zero-fill (the reference zero-fills with torch.zeros).
+ *   - Column sums are deterministic: each column is reduced by one
+ *     workgroup in a fixed order (the reference uses fp32 atomics).
  *
- * Return value: FAS_OK (0) or a negative fas_status_t; fas_last_error()
- * then returns a thread-local message naming the entry point and the cause.
+ * Return value: FAS_OK (0) or a negative fas_status; fas_last_error() then
+ * returns a thread-local message naming the entry point and the cause.
  */
 #ifndef FAS_H_
 #define FAS_H_
@@ -41,7 +45,7 @@
 extern "C" {
 #endif
 
-#define FAS_ABI_VERSION 1
+#define FAS_ABI_VERSION 2
 
 typedef enum fas_dtype {
   FAS_DTYPE_F16 = 0,
@@ -52,9 +56,21 @@ typedef enum fas_status {
   FAS_OK = 0,
   FAS_ERR_INVALID = -1,     /* bad shape, pointer, stride or alignment */
   FAS_ERR_UNSUPPORTED = -2, /* valid request this build does not implement */
-  FAS_ERR_WORKSPACE = -3,   /* caller-provided scratch too small */
+  FAS_ERR_WORKSPACE = -3,   /* caller-provided workspace too small */
   FAS_ERR_HIP = -4          /* the HIP runtime rejected a launch */
 } fas_status;
+
+/* Variant selector for fas_workspace_bytes. */
+typedef enum fas_variant {
+  FAS_VARIANT_SCORES = 0,
+  FAS_VARIANT_ROW_SUM = 1,
+  FAS_VARIANT_COL_SUM = 2,
+  FAS_VARIANT_COL_SUM_SEQUENTIAL = 3,
+  FAS_VARIANT_SOFTMAX_COL_SUM = 4,
+  FAS_VARIANT_CROSS_QK_SUM = 5,
+  FAS_VARIANT_CROSS_SOFTMAX_SUM = 6,
+  FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7
+} fas_variant;
 
 /* The attention problem shared by every entry point.  Strides are in
  * elements, ordered (batch, head, row, dim); stride[3] must be 1. */
@@ -72,11 +88,6 @@ typedef struct fas_attn_args {
   int64_t k_stride[4];
   int64_t v_stride[4];
   int64_t out_stride[4];
-  /* Optional natural-log LSE per query row, (B, Hq, M) fp32 with strides
-   * lse_stride (batch, head, row); NULL to skip.  The reference computes it
-   * (attention_with_scores.py:191-211) but no launcher returns it. */
-  float* lse;
-  int64_t lse_stride[3];
 } fas_attn_args;
 
 int fas_abi_version(void);
@@ -84,11 +95,15 @@ int fas_abi_version(void);
 /* Thread-local description of the last failure on this thread ("" if none). */
 const char* fas_last_error(void);
 
+/* Device workspace (bytes, 256-byte aligned) an entry point of `variant`
+ * needs for this problem; 0 when it needs none.  split is ignored by the
+ * variants without one.  Returns (size_t)-1 for an invalid request. */
+size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split);
+
 /* Replaces attention_with_scores.py:214-333 (+ _fwd_kernel_with_scores
  * :23-211).  scores is (B, Hq, M, N) in the input dtype with element strides
  * scores_stride (innermost 1); it receives (q.k) * sm_scale, with masked
- * positions (causal, upper triangle) written as 0.  The whole matrix is
- * written by the kernel, so the caller need not zero it. */
+ * positions (causal, upper triangle) written as 0 by the kernel itself. */
 int fas_attention_with_scores(const fas_attn_args* a, void* scores,
                               const int64_t scores_stride[4], void* stream);
 
@@ -98,57 +113,52 @@ int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum,
                                const int64_t row_sum_stride[3], void* stream);
 
 /* Replaces attention_with_col_sum.py:297-419 (+ kernel :22-294): col_sum is
- * (B, Hk, N) fp32, sum over queries and group heads of (q.k)*sm_scale.  Key
- * tiles are visited in reverse order when causal, round-robin otherwise. */
+ * (B, Hk, N) fp32, sum over admissible queries and group heads of
+ * (q.k)*sm_scale.  The reference's reverse / round-robin key orders only
+ * change its atomic summation order; this result is order-independent. */
 int fas_attention_with_col_sum(const fas_attn_args* a, float* col_sum,
-                               const int64_t col_sum_stride[3], void* stream);
+                               const int64_t col_sum_stride[3], void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* Replaces attention_with_col_sum_sequential.py:214-341 (+ kernel :23-211):
- * same output as fas_attention_with_col_sum, round-robin key order. */
+ * same output as fas_attention_with_col_sum. */
 int fas_attention_with_col_sum_sequential(const fas_attn_args* a, float* col_sum,
-                                          const int64_t col_sum_stride[3],
-                                          void* stream);
+                                          const int64_t col_sum_stride[3], void* workspace,
+                                          size_t workspace_bytes, void* stream);
 
 /* Replaces attention_with_col_softmax_sum.py:274-401 (+ kernel :23-270):
  * col_sum is (B, Hk, N) fp32, sum over queries and group heads of the final
- * softmax weights P = exp(s - m) / l.  Two passes over K; the second pass
- * visits key tiles in reverse order when causal. */
+ * softmax weights P = exp(s - m) / l.  Second pass key-block outer. */
 int fas_attention_with_softmax_col_sum(const fas_attn_args* a, float* col_sum,
-                                       const int64_t col_sum_stride[3],
-                                       void* stream);
+                                       const int64_t col_sum_stride[3], void* workspace,
+                                       size_t workspace_bytes, void* stream);
 
 /* Replaces attention_cross_token_qk_sum.py:255-408 (+ kernel :17-252):
  * cross is (B, Hk, split) fp32, sum over queries i >= split of (q.k)*sm_scale
  * for keys j < split.  Causal masking here (and for out) is top-left:
  * i >= j.  0 < split <= N. */
-int fas_attention_cross_token_qk_sum(const fas_attn_args* a, int64_t split,
-                                     float* cross, const int64_t cross_stride[3],
-                                     void* stream);
+int fas_attention_cross_token_qk_sum(const fas_attn_args* a, int64_t split, float* cross,
+                                     const int64_t cross_stride[3], void* workspace,
+                                     size_t workspace_bytes, void* stream);
 
 /* Replaces attention_cross_token_softmax_sum.py:735-863 (+ fused kernel
  * :24-268): cross is (B, Hk, split) fp32, sum over queries i >= split of the
  * softmax weights exp(s - m) / (l + 1e-12) for keys j < split. */
-int fas_attention_cross_token_softmax_sum(const fas_attn_args* a, int64_t split,
-                                          float* cross,
-                                          const int64_t cross_stride[3],
-                                          void* stream);
-
-/* Bytes of scratch fas_attention_cross_token_softmax_sum_buffered needs:
- * the fp32 raw scores of the (i >= split, j < split) region,
- * B * Hq * max(M - split, 0) * split * 4.  The reference sizes its buffer
- * B * Hq * M * N * 4 (attention_cross_token_softmax_sum.py:704-705); only
- * the region is ever re-read, so only the region is kept. */
-size_t fas_cross_token_softmax_sum_buffered_workspace_bytes(
-    const fas_attn_args* a, int64_t split);
+int fas_attention_cross_token_softmax_sum(const fas_attn_args* a, int64_t split, float* cross,
+                                          const int64_t cross_stride[3], void* workspace,
+                                          size_t workspace_bytes, void* stream);
 
 /* Replaces attention_cross_token_softmax_sum.py:639-732 (+ buffered kernel
- * :434-636): same output as fas_attention_cross_token_softmax_sum, but pass 1
- * stores the raw fp32 scores of the region in workspace and pass 2 reloads
- * them instead of recomputing q.k. */
-int fas_attention_cross_token_softmax_sum_buffered(
-    const fas_attn_args* a, int64_t split, float* cross,
-    const int64_t cross_stride[3], void* workspace, size_t workspace_bytes,
-    void* stream);
+ * :434-636): same output as fas_attention_cross_token_softmax_sum, but the
+ * first pass stores the raw fp32 scores of the region (rows >= split, keys
+ * < split) in the workspace and the second pass reloads them instead of
+ * recomputing q.k.  The reference sizes its buffer B*Hq*M*N*4 bytes
+ * (attention_cross_token_softmax_sum.py:704-705); only the region,
+ * B*Hq*(M - split)*split*4 bytes, is ever re-read, so only it is kept. */
+int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64_t split,
+                                                   float* cross, const int64_t cross_stride[3],
+                                                   void* workspace, size_t workspace_bytes,
+                                                   void* stream);
 
 #ifdef __cplusplus
 }
