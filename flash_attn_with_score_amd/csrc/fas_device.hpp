@@ -69,6 +69,42 @@ __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float log2f_fast(float x) { return __builtin_amdgcn_logf(x); }
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor as four SGPR words for inline assembly.
+__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return i32x4{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, kRsrcWord3};
+}
+
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)((const FAS_LDS void*)p);
+}
+
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// Direct global -> LDS copy of 16 bytes per lane: lane l's bytes land at
+// LDS byte address lds_base + 16*l (lds_base wave-uniform); out-of-range
+// offsets write zeros.  Issued from inline assembly so the compiler neither
+// tracks it nor inserts waits for it: the caller waits with vm_wait_all().
+__device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds_base), "v"(voff), "s"(rsrc)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ void vm_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Workgroup barrier ordering LDS only.  __syncthreads() is also a release
+// fence for global memory, which makes every wave drain its outstanding
+// global stores at each barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Raw buffer over [base, base + bytes): loads past the end return 0, stores
 // past the end are dropped.  Offsets are 32-bit byte offsets.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {

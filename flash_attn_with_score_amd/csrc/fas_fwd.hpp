@@ -59,6 +59,42 @@ __device__ __forceinline__ void map_block(int bid, int nrb, int BH, bool causal,
   if (causal) rb = nrb - 1 - rb;
 }
 
+// Zero writer for the never-computed causal part of 32 score rows: keys
+// [z0, N) of rows [rbase, rbase + 32) of the workgroup's row block, walked
+// in row-major 16-byte chunks, `quota` wave-wide stores per call.
+struct ZeroFill {
+  int row = 0, col = 0, step_r = 0, step_c = 0, cpr = 0, left = 0, quota = 0, z0 = 0, rbase = 0;
+
+  __device__ __forceinline__ void init(int N, int wtiles, int rbase_, int rows_valid, int lane,
+                                       int ntiles) {
+    rbase = rbase_;
+    z0 = wtiles * 64;
+    cpr = (N - z0) / 8;
+    left = 0;
+    if (cpr > 0 && rows_valid > 0) {
+      left = (32 * cpr + 63) / 64;
+      quota = (left + max(ntiles, 1) - 1) / max(ntiles, 1);
+      row = lane / cpr;
+      col = lane % cpr;
+      step_r = 64 / cpr;
+      step_c = 64 % cpr;
+    }
+  }
+  __device__ __forceinline__ void run(int count, __amdgpu_buffer_rsrc_t rs, int64_t ss2) {
+    for (int u = 0; u < count && left > 0; ++u, --left) {
+      if (row < 32)
+        buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rs,
+                       (uint32_t)(((rbase + row) * ss2 + z0 + 8 * col) * 2));
+      row += step_r;
+      col += step_c;
+      if (col >= cpr) {
+        col -= cpr;
+        ++row;
+      }
+    }
+  }
+};
+
 template <class E, int D, int MODE, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(const FwdParams p) {
@@ -66,16 +102,30 @@ void fwd_kernel(const FwdParams p) {
   constexpr int DB = (D + 31) / 32;        // 32-dim blocks of O^T
   constexpr int BM = 32 * NW;
   constexpr int BN = 64;
-  constexpr int NT = NW * 64;
   constexpr int TILE = BN * D;             // elements per K or V tile
-  constexpr int CHUNKS = TILE / 8;         // 16-byte chunks per tile
-  constexpr int CPT = (CHUNKS + NT - 1) / NT;
-  constexpr int CPR = D / 8;               // chunks per row
+  constexpr int BLOCKS = TILE / 512;       // 1 KiB DMA blocks per tile
+  constexpr int RPB = 512 / D;             // tile rows per DMA block
+  constexpr int CPR = D / 8;               // 16-byte chunks per row
+  // Score writer with 8 waves: waves 0-3 fetch K/V and stage their score
+  // tiles in LDS; waves 4-7 never load inside the loop and issue every
+  // global score store (their own and their partner's) plus the zero
+  // triangle, so no wave ever waits for a store to finish.
+  constexpr bool kSplit = MODE == kFwdScores && NW == 8;
+  constexpr int NL = kSplit ? 4 : NW;      // waves issuing tile loads
+  constexpr int QPW = (BLOCKS + NL - 1) / NL;
+  // Score tiles leave through LDS (4 KiB per 32-row wave tile), so that
+  // every global store instruction writes 8 full 128-byte row segments.
+  // Split mode: 2 stages x 4 loader tiles, then one tile per storer.
+  constexpr int TSZ = 256;  // 16-byte units per wave tile
+  constexpr int SG = MODE != kFwdScores ? 1 : (kSplit ? (8 + 4) * TSZ : NW * TSZ);
 
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t kv[2][2][TILE];
+  __shared__ __attribute__((aligned(16))) u32x4 stg[SG];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const bool loader = !kSplit || wave < 4;
 
   int rb, bh;
   map_block(blockIdx.x, p.nrb, p.B * p.H, p.causal != 0, rb, bh);
@@ -85,19 +135,21 @@ void fwd_kernel(const FwdParams p) {
   const int qrow = wrow0 + c;
 
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
-  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
-  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + b * p.sv0 + hk * p.sv1, p.v_bytes);
+  const i32x4 wk = make_rsrc_words(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
+  const i32x4 wv = make_rsrc_words(p.v + b * p.sv0 + hk * p.sv1, p.v_bytes);
+  const uint32_t kv_base = lds_addr(&kv[0][0][0]);
 
-  // Key range: the workgroup visits tiles [0, ntiles); this wave computes
-  // tiles [0, wtiles) and tiles [0, tfull) need no mask.
-  int hi = p.N, whi = p.N, tfull = p.N / BN;
-  if (p.causal) {
-    hi = min(p.N, max(0, p.causal_off + row0 + BM));
-    whi = min(p.N, max(0, p.causal_off + wrow0 + 32));
-    tfull = min(tfull, max(0, p.causal_off + wrow0 + 1) / BN);
-  }
+  // Key range of a wave starting at row r: tiles [0, wt(r)) are computed,
+  // tiles [0, tf(r)) need no mask.
+  auto wtiles_of = [&](int r) {
+    const int whi = p.causal ? min(p.N, max(0, p.causal_off + r + 32)) : p.N;
+    return (whi + BN - 1) / BN;
+  };
+  const int hi = p.causal ? min(p.N, max(0, p.causal_off + row0 + BM)) : p.N;
   const int ntiles = (hi + BN - 1) / BN;
-  const int wtiles = (whi + BN - 1) / BN;
+  const int wtiles = wtiles_of(wrow0);
+  int tfull = p.N / BN;
+  if (p.causal) tfull = min(tfull, max(0, p.causal_off + wrow0 + 1) / BN);
 
   // Q (B operand of S^T = K Q^T): lane holds Q[qrow][16ks + 8g, +8).
   u32x4 qreg[KS];
@@ -105,65 +157,76 @@ void fwd_kernel(const FwdParams p) {
   for (int ks = 0; ks < KS; ++ks)
     qreg[ks] = buf_load16(rq, (uint32_t)((qrow * p.sq2 + 16 * ks + 8 * g) * 2)) ^ p.qneg;
 
-  // Tile staging: thread chunk i -> (row, ch).
-  u32x4 kst[CPT], vst[CPT];
-  auto fetch = [&](int t) {
+  // Tile t -> LDS stage: block q of K (and of V) is rows [q*RPB, +RPB);
+  // lane l fills physical chunk l % CPR of row q*RPB + l / CPR.
+  auto issue_tile = [&](int t, int stage) {
+    if (!loader) return;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int id = tid + i * NT;
-      const int row = id / CPR, ch = id % CPR;
-      const int key = t * BN + row;
-      kst[i] = buf_load16(rk, (uint32_t)((key * p.sk2 + ch * 8) * 2));
-      vst[i] = buf_load16(rv, (uint32_t)((key * p.sv2 + ch * 8) * 2));
-    }
-  };
-  auto stash = [&](int stage) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int id = tid + i * NT;
-      if (CHUNKS % NT == 0 || id < CHUNKS) {
-        const int row = id / CPR, ch = id % CPR;
-        *reinterpret_cast<u32x4*>(&lds[stage][0][tile_off<D>(row, ch)]) = kst[i];
-        *reinterpret_cast<u32x4*>(&lds[stage][1][tile_off<D>(row, ch)]) = vst[i];
+    for (int i = 0; i < QPW; ++i) {
+      const int q = wave + i * NL;
+      if (BLOCKS % NL == 0 || q < BLOCKS) {
+        const int row = q * RPB + lane / CPR;
+        const int ch = (lane % CPR) ^ swz<D>(row);
+        const int key = t * BN + row;
+        const uint32_t lb = kv_base + (uint32_t)((stage * 2 * TILE + q * 512) * 2);
+        dma16(wk, (uint32_t)((key * p.sk2 + ch * 8) * 2), __builtin_amdgcn_readfirstlane(lb));
+        dma16(wv, (uint32_t)((key * p.sv2 + ch * 8) * 2),
+              __builtin_amdgcn_readfirstlane(lb + TILE * 2));
       }
     }
   };
 
   // Score-matrix writer (kFwdScores).  Rows past M fall outside the buffer.
   __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scores, 0);
-  int zrow = 0, zcol = 0, zstep_r = 0, zstep_c = 0, zcpr = 0, zleft = 0, zquota = 0;
+  ZeroFill zf_own, zf_partner;
+  const int pwave = wave - 4;  // split mode: the loader wave a storer serves
+  const int prow0 = row0 + 32 * pwave;
+  const int pwtiles = kSplit ? wtiles_of(prow0) : 0;
   if constexpr (MODE == kFwdScores) {
     const int64_t base = b * p.ss0 + h * p.ss1 + (int64_t)row0 * p.ss2;
     const int rows = max(0, min(BM, p.M - row0));
     rs = make_rsrc(p.scores + base, (uint32_t)(rows * p.ss2 * 2));
-    // Zero region of this wave: rows [wrow0, wrow0 + 32), keys [wtiles*64, N).
-    const int z0 = wtiles * BN;
-    zcpr = (p.N - z0) / 8;  // 16-byte chunks per row (N % 8 == 0 on this path)
-    if (p.vec_scores && zcpr > 0 && wrow0 < p.M) {
-      const int total = 32 * zcpr;
-      zleft = (total + 63) / 64;  // wave-wide store instructions
-      zquota = (zleft + max(ntiles, 1) - 1) / max(ntiles, 1);
-      zrow = lane / zcpr;
-      zcol = lane % zcpr;
-      zstep_r = 64 / zcpr;
-      zstep_c = 64 % zcpr;
+    if (p.vec_scores && (!kSplit || !loader)) {
+      zf_own.init(p.N, wtiles, 32 * wave, p.M - wrow0, lane, ntiles);
+      if (kSplit) zf_partner.init(p.N, pwtiles, 32 * pwave, p.M - prow0, lane, ntiles);
     }
   }
-  auto zero_fill = [&](int count) {
+  auto zero_fill = [&]() {
     if constexpr (MODE == kFwdScores) {
-      const int z0 = wtiles * BN;
-      for (int u = 0; u < count && zleft > 0; ++u, --zleft) {
-        if (zrow < 32) {
-          const uint32_t off = (uint32_t)(((32 * wave + zrow) * p.ss2 + z0 + 8 * zcol) * 2);
-          buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rs, off);
-        }
-        zrow += zstep_r;
-        zcol += zstep_c;
-        if (zcol >= zcpr) {
-          zcol -= zcpr;
-          ++zrow;
-        }
-      }
+      zf_own.run(zf_own.quota, rs, p.ss2);
+      if constexpr (kSplit) zf_partner.run(zf_partner.quota, rs, p.ss2);
+    }
+  };
+  // Staged score tile: row r (32 rows), 16-byte chunk ch (8 per row) at
+  // unit r*8 + (ch ^ ((r >> 1) & 7)): conflict-free both for the MFMA-layout
+  // writes (16 rows, one chunk) and the row-major reads (2 rows, 8 chunks).
+  auto stage_tile = [&](int base, const f32x16 (&sv)[2]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f32x16& x = sv[j >> 1];
+      const int r0 = 8 * (j & 1);
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = x[r0 + e] == neg_inf() ? 0.f : x[r0 + e] * p.sm_scale;
+      stg[base + c * 8 + ((2 * j + g) ^ ((c >> 1) & 7))] =
+          u32x4{E::pack(v[0], v[1]), E::pack(v[2], v[3]), E::pack(v[4], v[5]),
+                E::pack(v[6], v[7])};
+    }
+  };
+  auto store_tile = [&](int base, int rbase, int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 8 * i + (lane >> 3), ch = lane & 7;
+      const u32x4 w = stg[base + r * 8 + (ch ^ ((r >> 1) & 7))];
+      const int key0 = k0 + 8 * ch;
+      if (key0 < p.N) buf_store16(w, rs, (uint32_t)(((rbase + r) * p.ss2 + key0) * 2));
+    }
+  };
+  // Storer side of split mode: the partner's staged score tile t.
+  auto flush_partner = [&](int t) {
+    if constexpr (kSplit) {
+      if (!loader && p.vec_scores && t >= 0 && t < pwtiles)
+        store_tile(((t & 1) * 4 + pwave) * TSZ, 32 * pwave, t * BN);
     }
   };
 
@@ -172,18 +235,16 @@ void fwd_kernel(const FwdParams p) {
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = f32x16{};
 
-  if (ntiles > 0) {
-    fetch(0);
-    stash(0);
-  }
-  __syncthreads();
+  if (ntiles > 0) issue_tile(0, 0);
+  if (loader) vm_wait_all();
+  lds_barrier();
 
   for (int it = 0; it < ntiles; ++it) {
     const int stage = it & 1;
-    const bool more = it + 1 < ntiles;
-    if (more) fetch(it + 1);
-    const uint16_t* kt = lds[stage][0];
-    const uint16_t* vt = lds[stage][1];
+    if (it + 1 < ntiles) issue_tile(it + 1, stage ^ 1);
+    flush_partner(it - 1);
+    const uint16_t* kt = kv[stage][0];
+    const uint16_t* vt = kv[stage][1];
     const int k0 = it * BN;
 
     if (it < wtiles) {
@@ -195,7 +256,7 @@ void fwd_kernel(const FwdParams p) {
         s[0] = E::mma(a0, qreg[ks], s[0]);
         s[1] = E::mma(a1, qreg[ks], s[1]);
       }
-      // Value index i = 16*kb + r holds key k0 + 32*kb + acc_row(r, g).
+      // Register r of s[kb] holds key k0 + 32*kb + acc_row(r, g).
       if (it >= tfull) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -209,21 +270,13 @@ void fwd_kernel(const FwdParams p) {
 
       if constexpr (MODE == kFwdScores) {
         if (p.vec_scores) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const f32x16& sv = s[j >> 1];
-            const int r0 = 8 * (j & 1);
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const float x = sv[r0 + e];
-              v[e] = x == neg_inf() ? 0.f : x * p.sm_scale;
-            }
-            const u32x4 w = {E::pack(v[0], v[1]), E::pack(v[2], v[3]), E::pack(v[4], v[5]),
-                             E::pack(v[6], v[7])};
-            const int key0 = k0 + 16 * j + 8 * g;
-            if (key0 < p.N)
-              buf_store16_nt(w, rs, (uint32_t)(((32 * wave + c) * p.ss2 + key0) * 2));
+          if (kSplit && loader) {
+            stage_tile((stage * 4 + wave) * TSZ, s);
+          } else {
+            // A wave reads back its own LDS writes in order: no barrier.
+            const int base = kSplit ? (8 + pwave) * TSZ : wave * TSZ;
+            stage_tile(base, s);
+            store_tile(base, 32 * wave, k0);
           }
         } else if (qrow < p.M) {
           uint16_t* srow = p.scores + b * p.ss0 + h * p.ss1 + (int64_t)qrow * p.ss2;
@@ -237,7 +290,7 @@ void fwd_kernel(const FwdParams p) {
             }
         }
       }
-      zero_fill(zquota);
+      zero_fill();
       if constexpr (MODE == kFwdRowSum) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -303,13 +356,15 @@ void fwd_kernel(const FwdParams p) {
         for (int cs = 0; cs < 4; ++cs)
           oacc[db] = E::mma(lds_vt_operand<D>(vt, db, cs, lane), pb[cs], oacc[db]);
     } else {
-      zero_fill(zquota);
+      zero_fill();
     }
-    if (more) stash(stage ^ 1);
-    __syncthreads();
+    if (loader) vm_wait_all();
+    lds_barrier();
   }
-  zero_fill(1 << 30);
+  flush_partner(ntiles - 1);
   if constexpr (MODE == kFwdScores) {
+    zf_own.run(1 << 30, rs, p.ss2);
+    if constexpr (kSplit) zf_partner.run(1 << 30, rs, p.ss2);
     if (!p.vec_scores) {  // element-wise zero triangle for unaligned rows
       const int z0 = min(p.N, wtiles * BN);
       for (int rr = 0; rr < 32; ++rr) {

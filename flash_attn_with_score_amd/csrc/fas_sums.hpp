@@ -55,7 +55,8 @@ void colsm_kernel(const ColsmParams p) {
   __shared__ __attribute__((aligned(16))) float llds[2][TQ];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int lane = tid & 63, c = lane & 31, g = lane >> 5;
   int kb, bh;
   map_block_keys(blockIdx.x, p.nkb, p.B * p.H, kb, bh);
   const int h = bh % p.H, b = bh / p.H, hk = h / p.G;
