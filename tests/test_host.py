@@ -1,0 +1,233 @@
+"""Host-side tests of the boundary -- run without a GPU.
+
+  * libfas.so loads (built by __graft_entry__.build()) and exports exactly
+    the functions include/fas.h declares, with the ctypes signatures of
+    flash_attn_with_score_amd/_native.py;
+  * fas_workspace_bytes sizes each variant's workspace as documented;
+  * invalid requests are rejected with the right status and a message that
+    names the entry point, before any HIP call is made;
+  * the Python launchers keep the reference's asserts
+    (e.g. attention_with_scores.py:240-247, attention_cross_token_qk_sum.py:298-307)
+    and fail loudly instead of falling back to a CPU path;
+  * the product package never imports the test oracle.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import flash_attn_with_score_amd as fas
+from flash_attn_with_score_amd import _common, _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fas.h")
+
+SIZE_MAX = ctypes.c_size_t(-1).value
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _native.load()
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(fas_\w+)\s*\(", text, re.M))
+
+
+def test_library_loads_with_abi_version(lib):
+    assert lib.fas_abi_version() == _native.ABI_VERSION == 2
+
+
+def test_exports_match_header(lib):
+    declared = header_functions()
+    assert declared == set(_native.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_public_api_matches_reference_names():
+    """__init__.py:29-39 of the reference minus flash.attention."""
+    assert set(fas.__all__) == {
+        "attention_with_scores", "attention_with_row_sum", "attention_with_col_sum",
+        "attention_with_col_sum_sequential", "attention_with_softmax_col_sum",
+        "attention_cross_token_qk_sum", "attention_cross_token_softmax_sum",
+        "attention_cross_token_softmax_sum_buffered"}
+
+
+def make_args(B=1, Hq=4, Hk=2, M=300, N=300, D=128, causal=1, dtype=0, ptr=0x10000):
+    a = _native.AttnArgs()
+    a.dtype, a.causal, a.sm_scale = dtype, causal, 1.0 / (D ** 0.5)
+    a.batch, a.heads_q, a.heads_k, a.seqlen_q, a.seqlen_k, a.head_dim = B, Hq, Hk, M, N, D
+    a.q = a.k = a.v = a.out = ptr  # never dereferenced by the rejected calls below
+    for name, H, L in (("q_stride", Hq, M), ("k_stride", Hk, N), ("v_stride", Hk, N),
+                       ("out_stride", Hq, M)):
+        setattr(a, name, _native._I64x4(H * L * D, L * D, D, 1))
+    return a
+
+
+def test_workspace_sizes(lib):
+    B, Hq, Hk, M, N, D, split = 2, 8, 2, 300, 300, 64, 100
+
+    def r256(x):
+        return (x + 255) // 256 * 256
+
+    a = make_args(B, Hq, Hk, M, N, D)
+    ws = lambda v: lib.fas_workspace_bytes(v, ctypes.byref(a), split)  # noqa: E731
+    assert ws(_native.VARIANT_SCORES) == 0
+    assert ws(_native.VARIANT_ROW_SUM) == 0
+    nblk = (M + 63) // 64
+    assert ws(_native.VARIANT_COL_SUM) == r256(B * Hk * (nblk + 1) * D * 4)
+    assert ws(_native.VARIANT_COL_SUM_SEQUENTIAL) == ws(_native.VARIANT_COL_SUM)
+    assert ws(_native.VARIANT_SOFTMAX_COL_SUM) == r256(B * Hq * M * 4) + r256(B * Hq * N * 4)
+    assert ws(_native.VARIANT_CROSS_QK_SUM) == r256(B * Hk * ((M - split + 63) // 64 + 1) * D * 4)
+    assert ws(_native.VARIANT_CROSS_SOFTMAX_SUM) == r256(B * Hq * M * 4) + r256(B * Hq * split * 4)
+    assert ws(_native.VARIANT_CROSS_SOFTMAX_SUM_BUFFERED) == (
+        r256(B * Hq * M * 4) + r256(B * Hq * split * 4) + r256(B * Hq * (M - split) * split * 4))
+    # MHA needs no per-query-head partials.
+    a1 = make_args(B, 4, 4, M, N, D)
+    assert lib.fas_workspace_bytes(_native.VARIANT_SOFTMAX_COL_SUM, ctypes.byref(a1), 0) == \
+        r256(B * 4 * M * 4)
+
+
+def test_workspace_rejects_bad_requests(lib):
+    a = make_args()
+    assert lib.fas_workspace_bytes(_native.VARIANT_CROSS_QK_SUM, ctypes.byref(a), 0) == SIZE_MAX
+    assert lib.fas_workspace_bytes(_native.VARIANT_CROSS_QK_SUM, ctypes.byref(a), 301) == SIZE_MAX
+    assert lib.fas_workspace_bytes(99, ctypes.byref(a), 1) == SIZE_MAX
+    bad = make_args(D=48)
+    assert lib.fas_workspace_bytes(_native.VARIANT_COL_SUM, ctypes.byref(bad), 0) == SIZE_MAX
+
+
+def _err(lib):
+    return _native.last_error(lib)
+
+
+def test_rejects_unsupported_head_dim(lib):
+    a = make_args(D=48)
+    st = _native._I64x4(1, 1, 1, 1)
+    rc = lib.fas_attention_with_scores(ctypes.byref(a), 0x10000, st, None)
+    assert rc == _native.FAS_ERR_UNSUPPORTED
+    assert "fas_attention_with_scores" in _err(lib) and "head_dim 48" in _err(lib)
+
+
+def test_rejects_bad_heads_and_dtype(lib):
+    a = make_args(Hq=6, Hk=4)
+    st = _native._I64x3(1, 1, 1)
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert "multiple" in _err(lib)
+    a = make_args(dtype=7)
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == \
+        _native.FAS_ERR_UNSUPPORTED
+
+
+def test_rejects_null_and_misaligned_tensors(lib):
+    st = _native._I64x3(1, 1, 1)
+    a = make_args()
+    a.q = None
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert "q is NULL" in _err(lib)
+    a = make_args()
+    a.k_stride = _native._I64x4(2 * 300 * 128, 300 * 128, 130, 1)  # row stride not a multiple of 8
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert "k rows must be 16-byte aligned" in _err(lib)
+    a = make_args()
+    a.v_stride = _native._I64x4(2 * 300 * 128, 300 * 128, 128, 2)
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert "innermost stride" in _err(lib)
+
+
+def test_rejects_split_out_of_range(lib):
+    a = make_args()
+    st = _native._I64x3(1, 1, 1)
+    for split in (0, -3, 301):
+        rc = lib.fas_attention_cross_token_softmax_sum(ctypes.byref(a), split, 0x10000, st,
+                                                       0x10000, 1 << 30, None)
+        assert rc == _native.FAS_ERR_INVALID, split
+        assert "split" in _err(lib)
+
+
+def test_rejects_short_workspace(lib):
+    a = make_args()
+    st = _native._I64x3(1, 1, 1)
+    need = lib.fas_workspace_bytes(_native.VARIANT_SOFTMAX_COL_SUM, ctypes.byref(a), 0)
+    rc = lib.fas_attention_with_softmax_col_sum(ctypes.byref(a), 0x10000, st, 0x10000, need - 1,
+                                                None)
+    assert rc == _native.FAS_ERR_WORKSPACE and str(need) in _err(lib)
+    rc = lib.fas_attention_with_col_sum(ctypes.byref(a), 0x10000, st, None, 0, None)
+    assert rc == _native.FAS_ERR_WORKSPACE
+
+
+def test_error_code_maps_to_runtime_error():
+    class FakeLib:
+        @staticmethod
+        def fas_last_error():
+            return b"fas_attention_with_scores: HIP launch failed: out of memory"
+
+    with pytest.raises(RuntimeError, match="HIP launch failed: out of memory"):
+        _native.check(FakeLib(), _native.FAS_ERR_HIP, "fas_attention_with_scores")
+    _native.check(FakeLib(), _native.FAS_OK, "fas_attention_with_scores")
+
+
+# ------------------------------------------------------------ launchers
+
+def _cpu_qkv(D=64, H=4, Hk=4, Hv=None, M=32, N=32, dtype=torch.float16):
+    q = torch.zeros(1, H, M, D, dtype=dtype)
+    k = torch.zeros(1, Hk, N, D, dtype=dtype)
+    v = torch.zeros(1, Hv or Hk, N, D, dtype=dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize("fn", sorted(fas.__all__))
+def test_launcher_keeps_reference_asserts(fn):
+    f = getattr(fas, fn)
+    split = ("cross" in fn,)
+    args = (16,) if split[0] else ()
+    q, k, v = _cpu_qkv(D=48)
+    with pytest.raises(AssertionError):
+        f(q, k, v, *args)
+    q, k, v = _cpu_qkv(H=6, Hk=4)
+    with pytest.raises(AssertionError):
+        f(q, k, v, *args)
+    q, k, v = _cpu_qkv(Hk=2, Hv=4)
+    with pytest.raises(AssertionError):
+        f(q, k, v, *args)
+    if split[0]:
+        q, k, v = _cpu_qkv()
+        with pytest.raises(AssertionError):
+            f(q, k, v, 0)
+        with pytest.raises(AssertionError):
+            f(q, k, v, 33)
+
+
+@pytest.mark.parametrize("fn", sorted(fas.__all__))
+def test_launcher_fails_loudly_without_device(fn):
+    """No CPU fallback: host tensors are rejected, dropout > 0 is refused."""
+    f = getattr(fas, fn)
+    args = (16,) if "cross" in fn else ()
+    q, k, v = _cpu_qkv()
+    with pytest.raises(RuntimeError, match="HIP device"):
+        f(q, k, v, *args, causal=True)
+    with pytest.raises(NotImplementedError):
+        f(q, k, v, *args, causal=True, dropout_p=0.1)
+    with pytest.raises(AssertionError):
+        f(q.float(), k.float(), v.float(), *args)
+
+
+def test_package_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "flash_attn_with_score_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for name in files:
+            if name.endswith(".py"):
+                text = open(os.path.join(dirpath, name)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle", text, re.M), name
+
+
+def test_rows_aligned_helper():
+    x = torch.zeros(2, 3, 5, 64, dtype=torch.float16)
+    assert _common._rows_aligned(x)
+    assert not _common._rows_aligned(x[..., 1:])
