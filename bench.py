@@ -104,8 +104,8 @@ def cpu_model() -> str:
 
 def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float) -> dict:
     """Times the CPU oracle (oracle/naive.py, the checker) on whole heads of
-    the same workload until budget_s of work is done; the rate is scaled to
-    the heads actually computed."""
+    the same workload, cycling over the heads until budget_s of work is
+    done; the rate counts the heads actually computed."""
     from oracle import inputs, naive
 
     threads = os.cpu_count() or 1
@@ -116,7 +116,8 @@ def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float)
     offset = naive.ENTRY_POINT_OFFSET[ep]
     done = 0
     t0 = time.perf_counter()
-    for h in range(H):
+    while True:
+        h = done % H
         naive.reference_forward(q, k, v, causal=causal, causal_offset=offset, split=split,
                                 want=("out", side), heads=[h])
         done += 1
@@ -130,9 +131,34 @@ def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float)
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"oracle/naive.py fp32 on {done} of {H} heads of {ep} at the bench shape "
-                  f"({elapsed:.1f} s; {cpu_model()}, os.cpu_count()={threads})",
+        "sample": f"oracle/naive.py (fp32 restatement of reference_implementations.py) on "
+                  f"{done} head-passes ({done / H:.2f}x the {H}-head workload) of {ep} at the "
+                  f"bench shape, {elapsed:.1f} s; {cpu_model()}, os.cpu_count()={threads}",
     }
+
+
+# Measured HBM bytes per launch of the dominant kernel (two rocprofv3 PMC
+# passes, FETCH_SIZE and WRITE_SIZE scaled against a copy of known size),
+# recorded in a committed summary under profiles/ next to the command that
+# produced it.
+TRAFFIC_SUMMARIES = {
+    ("scores", 1, 32, 32, 4096, 128, "fp16", True): "attn_fwd_scores_f16_b1h32s4096d128_causal.md",
+}
+
+
+def measured_traffic(key):
+    name = TRAFFIC_SUMMARIES.get(key)
+    if name is None:
+        return None, None
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("TRAFFIC_BYTES_PER_LAUNCH"):
+                    return int(line.split("=")[1]), "profiles/" + name
+    except OSError:
+        pass
+    return None, None
 
 
 def make_call(fas, name, q, k, v, causal, split):
@@ -180,6 +206,9 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU-oracle work for cpu_baseline (0 disables)")
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run one 256 MiB device-to-device copy first (a kernel of known HBM "
+                         "traffic for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -205,6 +234,12 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.calibrate_copy:
+        src = torch.ones(128 << 20, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0, device=dev)
     call = make_call(fas, args.workload, q, k, v, causal, split)
     wall, dev_ms = time_steps(call, args.steps, args.warmup)
@@ -220,7 +255,10 @@ def main() -> int:
         achieved = flop / (dev_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4)}
-    roof["traffic"] = None
+    traffic, source = measured_traffic((args.workload, B, H, Hk, M, D, args.dtype, causal))
+    roof["traffic"] = traffic
+    if traffic is not None:
+        roof["traffic_source"] = source
     roof["kernel_ms"] = round(dev_ms, 4)
     roof["algorithmic_bytes"] = nbytes
     roof["algorithmic_flop"] = flop
