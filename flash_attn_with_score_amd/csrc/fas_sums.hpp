@@ -22,6 +22,8 @@
 #include "fas_device.hpp"
 #include "fas_params.hpp"
 
+#include <type_traits>
+
 namespace fas {
 
 // ---------------------------------------------------------------- softmax
@@ -123,7 +125,10 @@ void colsm_kernel(const ColsmParams p) {
       live = p.causal_off + r0 + TQ - 1 >= key0;
       full = p.causal_off + r0 >= key0 + KW - 1;
     }
-    if (live) {
+    // Both query blocks of the tile; the causal mask only on diagonal tiles
+    // (separate code, so full tiles carry no per-element test).
+    auto body = [&](auto mask_tag) __attribute__((always_inline)) {
+      constexpr bool MASK = decltype(mask_tag)::value;
       const uint16_t* qt = qlds[stage];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
@@ -146,20 +151,26 @@ void colsm_kernel(const ColsmParams p) {
         }
 #pragma unroll
         for (int kblk = 0; kblk < 2; ++kblk) {
-          const int key = key0 + 32 * kblk + c;
-          float acc = 0.f;
+          float pr[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            float pr = exp2f_fast(fmaf(s[kblk][r], p.qk_scale, -lr[r]));
-            if (!full) {
+            pr[r] = exp2f_fast(fmaf(s[kblk][r], p.qk_scale, -lr[r]));
+            if constexpr (MASK) {
               const int row = r0 + 32 * qb + acc_row(r, g);
-              if (p.causal_off + row < key) pr = 0.f;
+              if (p.causal_off + row < key0 + 32 * kblk + c) pr[r] = 0.f;
             }
-            acc += pr;
           }
-          colacc[kblk] += acc;
+#pragma unroll
+          for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+            for (int r = 0; r < w; ++r) pr[r] += pr[r + w];
+          colacc[kblk] += pr[0];
         }
       }
+    };
+    if (live) {
+      if (full) body(std::false_type{});
+      else body(std::true_type{});
     }
     if (more) stash(stage ^ 1);
     __syncthreads();
