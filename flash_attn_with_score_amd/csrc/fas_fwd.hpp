@@ -35,7 +35,8 @@
 //    key-length edge; all other tiles take an unmasked path.
 //  * The score-writing variant streams the causal zero triangle out in
 //    chunks interleaved with the compute loop, so each wave keeps the
-//    write queue busy while its MFMA work runs.
+//    write queue busy while its MFMA work runs; each workgroup writes the
+//    zeros of its mirror row block, which evens the write stream over time.
 #pragma once
 #include "fas_device.hpp"
 #include "fas_params.hpp"
@@ -60,38 +61,48 @@ __device__ __forceinline__ void map_block(int bid, int nrb, int BH, bool causal,
 }
 
 // Zero writer for the never-computed causal part of 32 score rows: keys
-// [z0, N) of rows [rbase, rbase + 32) of the workgroup's row block, walked
-// in row-major 16-byte chunks, `quota` wave-wide stores per call.
+// [z0, N) of rows [rbase, rbase + 32) of a row block.  Lane l covers chunks
+// l, l+64, ... of a row (16 bytes each), so each store instruction writes
+// 1 KiB contiguous; the row offset is wave-uniform (SGPR) and the lane's
+// column offset loop-invariant, so a store costs no vector arithmetic;
+// lanes past the row's last chunk use an offset beyond the buffer (dropped).
+// `rows_per_call` rows are written per call.
 struct ZeroFill {
-  int row = 0, col = 0, step_r = 0, step_c = 0, cpr = 0, left = 0, quota = 0, z0 = 0, rbase = 0;
+  int next = 32, nrows = 0, rows_per_call = 0, nfull = 0, rbase = 0;
+  uint32_t vbase = 0, vlast = 0;
+  bool has_last = false;
 
   __device__ __forceinline__ void init(int N, int wtiles, int rbase_, int rows_valid, int lane,
                                        int ntiles) {
     rbase = rbase_;
-    z0 = wtiles * 64;
-    cpr = (N - z0) / 8;
-    left = 0;
+    const int z0 = wtiles * 64;
+    const int cpr = (N - z0) / 8;  // chunks per row (N % 8 == 0 on this path)
+    next = 32;
+    // Only rows below M are written: the row offset travels in soffset, so
+    // the descriptor's range check is not relied on for rows.
+    nrows = min(32, rows_valid);
     if (cpr > 0 && rows_valid > 0) {
-      left = (32 * cpr + 63) / 64;
-      quota = (left + max(ntiles, 1) - 1) / max(ntiles, 1);
-      row = lane / cpr;
-      col = lane % cpr;
-      step_r = 64 / cpr;
-      step_c = 64 % cpr;
+      next = 0;
+      rows_per_call = (32 + max(ntiles, 1) - 1) / max(ntiles, 1);
+      nfull = cpr / 64;
+      const int rem = cpr % 64;
+      has_last = rem != 0;
+      vbase = (uint32_t)((z0 + 8 * lane) * 2);
+      // Lanes past the row's last chunk aim beyond the buffer: dropped.
+      vlast = lane < rem ? vbase + (uint32_t)(nfull * 1024) : 0x80000000u;
     }
   }
-  __device__ __forceinline__ void run(int count, __amdgpu_buffer_rsrc_t rs, int64_t ss2) {
-    for (int u = 0; u < count && left > 0; ++u, --left) {
-      if (row < 32)
-        buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rs,
-                       (uint32_t)(((rbase + row) * ss2 + z0 + 8 * col) * 2));
-      row += step_r;
-      col += step_c;
-      if (col >= cpr) {
-        col -= cpr;
-        ++row;
-      }
+  __device__ __forceinline__ void run(int rows, __amdgpu_buffer_rsrc_t rz, int64_t ss2) {
+    const int end = min(nrows, next + rows);
+    for (int r = next; r < end; ++r) {
+      const uint32_t soff = (uint32_t)((rbase + r) * ss2 * 2);
+      for (int j = 0; j < nfull; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rz, vbase + 1024u * j, soff,
+                                               kAuxNT);
+      if (has_last)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rz, vlast, soff, kAuxNT);
     }
+    next = max(next, end);
   }
 };
 
@@ -178,6 +189,12 @@ void fwd_kernel(const FwdParams p) {
 
   // Score-matrix writer (kFwdScores).  Rows past M fall outside the buffer.
   __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scores, 0);
+  // Zero triangle: a workgroup writes the never-computed part of its
+  // *mirror* row block nrb-1-rb (same head).  Row blocks with much compute
+  // have little zero area and vice versa, so every workgroup streams a
+  // similar share of zeros spread over its own iterations, and the HBM write
+  // stream stays even instead of arriving with the short blocks at the end.
+  __amdgpu_buffer_rsrc_t rz = rs;
   ZeroFill zf_own, zf_partner;
   const int pwave = wave - 4;  // split mode: the loader wave a storer serves
   const int prow0 = row0 + 32 * pwave;
@@ -186,28 +203,38 @@ void fwd_kernel(const FwdParams p) {
     const int64_t base = b * p.ss0 + h * p.ss1 + (int64_t)row0 * p.ss2;
     const int rows = max(0, min(BM, p.M - row0));
     rs = make_rsrc(p.scores + base, (uint32_t)(rows * p.ss2 * 2));
+    const int mrow0 = (p.nrb - 1 - rb) * BM;
+    const int mrows = max(0, min(BM, p.M - mrow0));
+    rz = make_rsrc(p.scores + b * p.ss0 + h * p.ss1 + (int64_t)mrow0 * p.ss2,
+                   (uint32_t)(mrows * p.ss2 * 2));
     if (p.vec_scores && (!kSplit || !loader)) {
-      zf_own.init(p.N, wtiles, 32 * wave, p.M - wrow0, lane, ntiles);
-      if (kSplit) zf_partner.init(p.N, pwtiles, 32 * pwave, p.M - prow0, lane, ntiles);
+      const int r_own = mrow0 + 32 * wave, r_par = mrow0 + 32 * pwave;
+      zf_own.init(p.N, wtiles_of(r_own), 32 * wave, p.M - r_own, lane, ntiles);
+      if (kSplit) zf_partner.init(p.N, wtiles_of(r_par), 32 * pwave, p.M - r_par, lane, ntiles);
     }
   }
   auto zero_fill = [&]() {
     if constexpr (MODE == kFwdScores) {
-      zf_own.run(zf_own.quota, rs, p.ss2);
-      if constexpr (kSplit) zf_partner.run(zf_partner.quota, rs, p.ss2);
+      zf_own.run(zf_own.rows_per_call, rz, p.ss2);
+      if constexpr (kSplit) zf_partner.run(zf_partner.rows_per_call, rz, p.ss2);
     }
   };
   // Staged score tile: row r (32 rows), 16-byte chunk ch (8 per row) at
   // unit r*8 + (ch ^ ((r >> 1) & 7)): conflict-free both for the MFMA-layout
   // writes (16 rows, one chunk) and the row-major reads (2 rows, 8 chunks).
-  auto stage_tile = [&](int base, const f32x16 (&sv)[2]) {
+  auto stage_tile = [&](int base, const f32x16 (&sv)[2], bool masked) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x16& x = sv[j >> 1];
       const int r0 = 8 * (j & 1);
       float v[8];
+      if (masked) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = x[r0 + e] == neg_inf() ? 0.f : x[r0 + e] * p.sm_scale;
+        for (int e = 0; e < 8; ++e) v[e] = x[r0 + e] == neg_inf() ? 0.f : x[r0 + e] * p.sm_scale;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = x[r0 + e] * p.sm_scale;
+      }
       stg[base + c * 8 + ((2 * j + g) ^ ((c >> 1) & 7))] =
           u32x4{E::pack(v[0], v[1]), E::pack(v[2], v[3]), E::pack(v[4], v[5]),
                 E::pack(v[6], v[7])};
@@ -271,11 +298,11 @@ void fwd_kernel(const FwdParams p) {
       if constexpr (MODE == kFwdScores) {
         if (p.vec_scores) {
           if (kSplit && loader) {
-            stage_tile((stage * 4 + wave) * TSZ, s);
+            stage_tile((stage * 4 + wave) * TSZ, s, it >= tfull);
           } else {
             // A wave reads back its own LDS writes in order: no barrier.
             const int base = kSplit ? (8 + pwave) * TSZ : wave * TSZ;
-            stage_tile(base, s);
+            stage_tile(base, s, it >= tfull);
             store_tile(base, 32 * wave, k0);
           }
         } else if (qrow < p.M) {
@@ -363,8 +390,8 @@ void fwd_kernel(const FwdParams p) {
   }
   flush_partner(ntiles - 1);
   if constexpr (MODE == kFwdScores) {
-    zf_own.run(1 << 30, rs, p.ss2);
-    if constexpr (kSplit) zf_partner.run(1 << 30, rs, p.ss2);
+    zf_own.run(32, rz, p.ss2);
+    if constexpr (kSplit) zf_partner.run(32, rz, p.ss2);
     if (!p.vec_scores) {  // element-wise zero triangle for unaligned rows
       const int z0 = min(p.N, wtiles * BN);
       for (int rr = 0; rr < 32; ++rr) {
