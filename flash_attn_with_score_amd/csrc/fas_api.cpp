@@ -39,15 +39,6 @@ bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u
 
 constexpr int64_t kMaxSliceBytes = (int64_t)1 << 31;
 
-// Waves per forward workgroup at head dim 128 (4 or 8; FAS_FWD_WAVES).
-int fwd_waves() {
-  static const int w = [] {
-    const char* e = std::getenv("FAS_FWD_WAVES");
-    return (e != nullptr && std::atoi(e) == 4) ? 4 : 8;
-  }();
-  return w;
-}
-
 // Checks one (B, H, L, D)-shaped 16-bit tensor: innermost stride 1, 16-byte
 // aligned rows, and a (batch, head) slice addressable with 32-bit offsets
 // (including the tile overhang the kernels read past the last row).
@@ -149,10 +140,9 @@ fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_le
   return p;
 }
 
-int run_fwd(const char* fn, fas::FwdParams& p, const Problem& pr, int mode, int waves, void* stream) {
+int run_fwd(const char* fn, fas::FwdParams& p, const Problem& pr, int mode, void* stream) {
   if (p.nrb == 0 || (int64_t)pr.B * pr.H == 0) return FAS_OK;
-  return hip_status(fn, fas::launch_fwd(p, mode, pr.dtype, pr.D, waves,
-                                        static_cast<hipStream_t>(stream)));
+  return hip_status(fn, fas::launch_fwd(p, mode, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
 }
 
 int check_out3(const char* fn, const char* name, const float* out, const int64_t* st) {
@@ -251,16 +241,15 @@ int run_raw(const char* fn, int variant, const fas_attn_args* a, int64_t split, 
   if ((rc = check_out3(fn, "sum output", out, st))) return rc;
   const int64_t ncols = ncols_of(variant, pr, split);
   if ((int64_t)pr.B * pr.Hk * ncols == 0) {
-    fas::FwdParams p = fwd_params(a, pr, cross, fas::fwd_rows_per_block(pr.D, fwd_waves()));
-    return run_fwd(fn, p, pr, fas::kFwdPlain, fwd_waves(), stream);
+    fas::FwdParams p = fwd_params(a, pr, cross, fas::kFwdRows);
+    return run_fwd(fn, p, pr, fas::kFwdPlain, stream);
   }
   const Workspace w = layout(variant, pr, split);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
 
   // Attention output.
-  const int waves = fwd_waves();
-  fas::FwdParams p = fwd_params(a, pr, cross, fas::fwd_rows_per_block(pr.D, waves));
-  if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, waves, stream))) return rc;
+  fas::FwdParams p = fwd_params(a, pr, cross, fas::kFwdRows);
+  if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, stream))) return rc;
   if (pr.M == 0) return zero_out3(fn, out, st, pr.B, pr.Hk, ncols, stream);
 
   fas::RawParams r{};
@@ -301,15 +290,14 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   const Workspace w = layout(variant, pr, split);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
 
-  const int waves = buffered ? 8 : fwd_waves();
-  fas::FwdParams p = fwd_params(a, pr, false, fas::fwd_rows_per_block(pr.D, waves));
+  fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   p.lse2 = at<float>(ws, w.lse);
   if (buffered) {
     p.region = at<float>(ws, w.region);
     p.split = (int)split;
     p.vec_region = (split % 4 == 0) ? 1 : 0;
   }
-  if ((rc = run_fwd(fn, p, pr, buffered ? fas::kFwdRegion : fas::kFwdPlain, waves, stream)))
+  if ((rc = run_fwd(fn, p, pr, buffered ? fas::kFwdRegion : fas::kFwdPlain, stream)))
     return rc;
   if ((int64_t)pr.B * pr.Hk * ncols == 0) return FAS_OK;
   if ((int64_t)pr.B * pr.H * pr.M == 0) return zero_out3(fn, out, st, pr.B, pr.Hk, ncols, stream);
@@ -382,8 +370,7 @@ int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_
   if (st[3] != 1) return fail(FAS_ERR_INVALID, fn, "scores innermost stride must be 1");
   if (reinterpret_cast<uintptr_t>(scores) & 1u)
     return fail(FAS_ERR_INVALID, fn, "scores is not 2-byte aligned");
-  const int waves = fwd_waves();
-  const int bm = fas::fwd_rows_per_block(pr.D, waves);
+  const int bm = fas::kFwdRows;
   if ((int64_t)bm * st[2] * 2 >= kMaxSliceBytes)
     return fail(FAS_ERR_UNSUPPORTED, fn, "score rows too long for 32-bit offsets");
   fas::FwdParams p = fwd_params(a, pr, false, bm);
@@ -393,7 +380,7 @@ int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_
   p.ss2 = st[2];
   p.vec_scores =
       aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && pr.N % 8 == 0;
-  return run_fwd(fn, p, pr, fas::kFwdScores, waves, stream);
+  return run_fwd(fn, p, pr, fas::kFwdScores, stream);
 }
 
 int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum, const int64_t st[3],
@@ -404,13 +391,12 @@ int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum, const int
   if ((rc = check_args(fn, a, &pr))) return rc;
   if ((int64_t)pr.B * pr.H * pr.M == 0) return FAS_OK;
   if ((rc = check_out3(fn, "row_sum", row_sum, st))) return rc;
-  const int waves = fwd_waves();
-  fas::FwdParams p = fwd_params(a, pr, false, fas::fwd_rows_per_block(pr.D, waves));
+  fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   p.aux = row_sum;
   p.sa0 = st[0];
   p.sa1 = st[1];
   p.sa2 = st[2];
-  return run_fwd(fn, p, pr, fas::kFwdRowSum, waves, stream);
+  return run_fwd(fn, p, pr, fas::kFwdRowSum, stream);
 }
 
 int fas_attention_with_col_sum(const fas_attn_args* a, float* col_sum, const int64_t st[3],

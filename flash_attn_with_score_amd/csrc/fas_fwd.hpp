@@ -18,7 +18,7 @@
 // Design (MI355X-first):
 //  * Workgroup = NW wave64s, 32 query rows per wave, BM = 32*NW rows; key
 //    tiles of 64.  K and V tiles are staged row-major in LDS (XOR-swizzled
-//    16-byte chunks), double-buffered: tile t+1 is fetched with buffer loads
+//    16-byte chunks), double-buffered: tile t+1 is fetched with LDS DMA
 //    (out-of-range keys read as 0) while tile t is consumed.
 //  * Scores are computed transposed, S^T = K Q^T (A = K rows from LDS,
 //    B = Q held in VGPRs), so lane l owns query row l%32 and 32 of the 64
@@ -33,13 +33,23 @@
 //    softmax (every term is divided by the same l at the end).
 //  * Masks are applied only on tiles that cross the causal diagonal or the
 //    key-length edge; all other tiles take an unmasked path.
-//  * The score-writing variant streams the causal zero triangle out in
-//    chunks interleaved with the compute loop, so each wave keeps the
-//    write queue busy while its MFMA work runs; each workgroup writes the
-//    zeros of its mirror row block, which evens the write stream over time.
+//  * Score writer (kFwdScores, 8 waves): waves 0-3 ("loaders") fetch K/V
+//    and never store inside the loop, so their wait for the DMA is never a
+//    wait for stores; waves 4-7 ("storers") issue every global score store.
+//    A CU can only drain stores at its share of HBM write bandwidth, and a
+//    wave that issues a store into a full queue stalls, so each storer
+//    spreads a fixed number of stores per key tile between its MFMAs
+//    (the partner's and its own staged tile of the previous key tile during
+//    S = K Q^T, zero slots during O += P V) instead of issuing them in
+//    bursts.
+//    Each workgroup writes the zeros of its *mirror* row block nrb-1-rb, so
+//    long-running workgroups carry the zeros of short ones and the write
+//    stream stays even over the kernel's life.
 #pragma once
 #include "fas_device.hpp"
 #include "fas_params.hpp"
+
+#include <type_traits>
 
 namespace fas {
 
@@ -60,55 +70,69 @@ __device__ __forceinline__ void map_block(int bid, int nrb, int BH, bool causal,
   if (causal) rb = nrb - 1 - rb;
 }
 
-// Zero writer for the never-computed causal part of 32 score rows: keys
-// [z0, N) of rows [rbase, rbase + 32) of a row block.  Lane l covers chunks
-// l, l+64, ... of a row (16 bytes each), so each store instruction writes
-// 1 KiB contiguous; the row offset is wave-uniform (SGPR) and the lane's
-// column offset loop-invariant, so a store costs no vector arithmetic;
-// lanes past the row's last chunk use an offset beyond the buffer (dropped).
-// `rows_per_call` rows are written per call.
-struct ZeroFill {
-  int next = 32, nrows = 0, rows_per_call = 0, nfull = 0, rbase = 0;
-  uint32_t vbase = 0, vlast = 0;
-  bool has_last = false;
+// Byte offset that every buffer access treats as out of range (dropped).
+constexpr uint32_t kOffNone = 0x80000000u;
 
-  __device__ __forceinline__ void init(int N, int wtiles, int rbase_, int rows_valid, int lane,
-                                       int ntiles) {
-    rbase = rbase_;
-    const int z0 = wtiles * 64;
-    const int cpr = (N - z0) / 8;  // chunks per row (N % 8 == 0 on this path)
-    next = 32;
-    // Only rows below M are written: the row offset travels in soffset, so
-    // the descriptor's range check is not relied on for rows.
-    nrows = min(32, rows_valid);
-    if (cpr > 0 && rows_valid > 0) {
-      next = 0;
-      rows_per_call = (32 + max(ntiles, 1) - 1) / max(ntiles, 1);
-      nfull = cpr / 64;
-      const int rem = cpr % 64;
-      has_last = rem != 0;
-      vbase = (uint32_t)((z0 + 8 * lane) * 2);
-      // Lanes past the row's last chunk aim beyond the buffer: dropped.
-      vlast = lane < rem ? vbase + (uint32_t)(nfull * 1024) : 0x80000000u;
-    }
+// Zero writer for the never-computed causal part of two 32-row rectangles of
+// a row block: rows [ra, ra + 32) x keys [za, N) and rows [rb, rb + 32) x
+// keys [zb, N) (row numbers relative to the block).  Store s of a rectangle
+// covers rows 8*(s & 3) .. +8 and keys 64*(s >> 2) .. +64: eight full
+// 128-byte row segments, lane l writing row l / 8, 16-byte chunk l % 8.
+// Every store is computed from wave-uniform values plus one lane constant,
+// so a slot costs a few scalar instructions and one vector select.
+struct ZeroJob {
+  int na = 0, nb = 0, next = 0;
+  int ra = 0, rb = 0, za = 0, zb = 0;
+
+  __device__ __forceinline__ static int count(int N, int z, int rows_valid) {
+    return (rows_valid > 0 && N > z) ? 4 * ((N - z + 63) >> 6) : 0;
   }
-  __device__ __forceinline__ void run(int rows, __amdgpu_buffer_rsrc_t rz, int64_t ss2) {
-    const int end = min(nrows, next + rows);
-    for (int r = next; r < end; ++r) {
-      const uint32_t soff = (uint32_t)((rbase + r) * ss2 * 2);
-      for (int j = 0; j < nfull; ++j)
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rz, vbase + 1024u * j, soff,
-                                               kAuxNT);
-      if (has_last)
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rz, vlast, soff, kAuxNT);
-    }
-    next = max(next, end);
+  __device__ __forceinline__ bool pending() const { return next < na + nb; }
+  // Byte offset of this lane's 16 bytes in store `next` (kOffNone when past
+  // the end of the job or past key N - 1), then advance.
+  __device__ __forceinline__ uint32_t take(uint32_t lane_off, int lane_key, int N, int ss2) {
+    const int s = next++;
+    const bool in_a = s < na;
+    const int loc = in_a ? s : s - na;
+    const int r = (in_a ? ra : rb) + 8 * (loc & 3);
+    const int k = (in_a ? za : zb) + 64 * (loc >> 2);
+    const bool ok = s < na + nb && k + lane_key < N;
+    return ok ? (uint32_t)((r * ss2 + k) * 2) + lane_off : kOffNone;
   }
 };
+
+// Scheduling hint for a storer's MFMA phase: alternate two MFMAs and one
+// global store, so each store finds room in the CU's store queue and the
+// wave never stalls on a burst.
+template <int N>
+__device__ __forceinline__ void interleave_mfma_stores() {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);  // VMEM write
+  }
+}
+
+// Schedule of one S^T = K Q^T tile (2 MFMAs and 2 operand fetches per
+// k-step): fetches run PD k-steps ahead of their MFMAs; NST global stores
+// of the same region go one per k-step.
+template <int KS, int NST>
+__device__ __forceinline__ void sched_score_tile() {
+  constexpr int PD = KS < 2 ? KS : 2;
+  __builtin_amdgcn_sched_group_barrier(0x100, 2 * PD, 0);  // DS read
+#pragma unroll
+  for (int i = 0; i < KS; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    if (i < NST) __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);  // VMEM write
+  }
+  if (NST > KS) __builtin_amdgcn_sched_group_barrier(0x040, NST > KS ? NST - KS : 1, 0);
+}
 
 template <class E, int D, int MODE, int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(const FwdParams p) {
+  static_assert(MODE != kFwdScores || NW == 8, "the score writer uses 8 waves");
   constexpr int KS = D / 16;               // MFMA k-steps over the head dim
   constexpr int DB = (D + 31) / 32;        // 32-dim blocks of O^T
   constexpr int BM = 32 * NW;
@@ -117,18 +141,16 @@ void fwd_kernel(const FwdParams p) {
   constexpr int BLOCKS = TILE / 512;       // 1 KiB DMA blocks per tile
   constexpr int RPB = 512 / D;             // tile rows per DMA block
   constexpr int CPR = D / 8;               // 16-byte chunks per row
-  // Score writer with 8 waves: waves 0-3 fetch K/V and stage their score
-  // tiles in LDS; waves 4-7 never load inside the loop and issue every
-  // global score store (their own and their partner's) plus the zero
-  // triangle, so no wave ever waits for a store to finish.
-  constexpr bool kSplit = MODE == kFwdScores && NW == 8;
+  constexpr bool kSplit = MODE == kFwdScores;
   constexpr int NL = kSplit ? 4 : NW;      // waves issuing tile loads
   constexpr int QPW = (BLOCKS + NL - 1) / NL;
   // Score tiles leave through LDS (4 KiB per 32-row wave tile), so that
-  // every global store instruction writes 8 full 128-byte row segments.
-  // Split mode: 2 stages x 4 loader tiles, then one tile per storer.
+  // every global store instruction writes 8 full 128-byte row segments:
+  // 2 stages x 4 loader tiles, then one tile per storer.
   constexpr int TSZ = 256;  // 16-byte units per wave tile
-  constexpr int SG = MODE != kFwdScores ? 1 : (kSplit ? (8 + 4) * TSZ : NW * TSZ);
+  constexpr int SG = kSplit ? (8 + 4) * TSZ : 1;
+  // Zero-store slots per key tile and storer (issued during O += P V).
+  constexpr int kZero = 8;
 
   __shared__ __attribute__((aligned(16))) uint16_t kv[2][2][TILE];
   __shared__ __attribute__((aligned(16))) u32x4 stg[SG];
@@ -170,7 +192,7 @@ void fwd_kernel(const FwdParams p) {
 
   // Tile t -> LDS stage: block q of K (and of V) is rows [q*RPB, +RPB);
   // lane l fills physical chunk l % CPR of row q*RPB + l / CPR.
-  auto issue_tile = [&](int t, int stage) {
+  auto issue_tile = [&](int t, int stage) __attribute__((always_inline)) {
     if (!loader) return;
 #pragma unroll
     for (int i = 0; i < QPW; ++i) {
@@ -187,42 +209,46 @@ void fwd_kernel(const FwdParams p) {
     }
   };
 
-  // Score-matrix writer (kFwdScores).  Rows past M fall outside the buffer.
+  // ---- score writer state (kFwdScores) ----
+  // Storers exist only for 16-byte aligned score rows; otherwise every wave
+  // writes its own scores element-wise.
+  const bool vec = MODE == kFwdScores && p.vec_scores != 0;
+  const bool storer = vec && !loader;
+  const int pwave = wave - 4;  // the loader wave a storer serves
+  const int pwtiles = kSplit ? wtiles_of(row0 + 32 * pwave) : 0;
+  const int ss2 = (int)p.ss2;
+  // Lane (row l/8, chunk l%8) of an 8-row x 128-byte store.
+  const int lane_key = 8 * (lane & 7);
+  const uint32_t lane_off = (uint32_t)(((lane >> 3) * ss2 + lane_key) * 2);
   __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scores, 0);
-  // Zero triangle: a workgroup writes the never-computed part of its
-  // *mirror* row block nrb-1-rb (same head).  Row blocks with much compute
-  // have little zero area and vice versa, so every workgroup streams a
-  // similar share of zeros spread over its own iterations, and the HBM write
-  // stream stays even instead of arriving with the short blocks at the end.
   __amdgpu_buffer_rsrc_t rz = rs;
-  ZeroFill zf_own, zf_partner;
-  const int pwave = wave - 4;  // split mode: the loader wave a storer serves
-  const int prow0 = row0 + 32 * pwave;
-  const int pwtiles = kSplit ? wtiles_of(prow0) : 0;
+  ZeroJob zj;
   if constexpr (MODE == kFwdScores) {
     const int64_t base = b * p.ss0 + h * p.ss1 + (int64_t)row0 * p.ss2;
     const int rows = max(0, min(BM, p.M - row0));
-    rs = make_rsrc(p.scores + base, (uint32_t)(rows * p.ss2 * 2));
+    // Extents pass through readfirstlane: the clamps may be computed on the
+    // vector ALU, and a descriptor in VGPRs costs a loop around every store.
+    rs = make_rsrc(p.scores + base, __builtin_amdgcn_readfirstlane((uint32_t)(rows * p.ss2 * 2)));
+    // Zeros of the mirror row block; rows past M fall outside rz.
     const int mrow0 = (p.nrb - 1 - rb) * BM;
     const int mrows = max(0, min(BM, p.M - mrow0));
     rz = make_rsrc(p.scores + b * p.ss0 + h * p.ss1 + (int64_t)mrow0 * p.ss2,
-                   (uint32_t)(mrows * p.ss2 * 2));
-    if (p.vec_scores && (!kSplit || !loader)) {
-      const int r_own = mrow0 + 32 * wave, r_par = mrow0 + 32 * pwave;
-      zf_own.init(p.N, wtiles_of(r_own), 32 * wave, p.M - r_own, lane, ntiles);
-      if (kSplit) zf_partner.init(p.N, wtiles_of(r_par), 32 * pwave, p.M - r_par, lane, ntiles);
+                   __builtin_amdgcn_readfirstlane((uint32_t)(mrows * p.ss2 * 2)));
+    if (storer) {
+      const int wa = wtiles_of(mrow0 + 32 * wave), wb = wtiles_of(mrow0 + 32 * pwave);
+      zj.ra = 32 * wave;
+      zj.rb = 32 * pwave;
+      zj.za = wa * BN;
+      zj.zb = wb * BN;
+      zj.na = ZeroJob::count(p.N, zj.za, p.M - (mrow0 + 32 * wave));
+      zj.nb = ZeroJob::count(p.N, zj.zb, p.M - (mrow0 + 32 * pwave));
     }
   }
-  auto zero_fill = [&]() {
-    if constexpr (MODE == kFwdScores) {
-      zf_own.run(zf_own.rows_per_call, rz, p.ss2);
-      if constexpr (kSplit) zf_partner.run(zf_partner.rows_per_call, rz, p.ss2);
-    }
-  };
   // Staged score tile: row r (32 rows), 16-byte chunk ch (8 per row) at
   // unit r*8 + (ch ^ ((r >> 1) & 7)): conflict-free both for the MFMA-layout
   // writes (16 rows, one chunk) and the row-major reads (2 rows, 8 chunks).
-  auto stage_tile = [&](int base, const f32x16 (&sv)[2], bool masked) {
+  auto stage_tile = [&](int base, const f32x16 (&sv)[2], bool masked)
+                        __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const f32x16& x = sv[j >> 1];
@@ -240,20 +266,41 @@ void fwd_kernel(const FwdParams p) {
                 E::pack(v[6], v[7])};
     }
   };
-  auto store_tile = [&](int base, int rbase, int k0) {
+  // Rows 8i + l/8, chunk l%8 of a staged tile, and their global offsets
+  // (rows rbase.. of the row block, keys k0..; kOffNone when !valid or past
+  // key N - 1).
+  auto read_staged = [&](int base, u32x4 (&w)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 8 * i + (lane >> 3), ch = lane & 7;
-      const u32x4 w = stg[base + r * 8 + (ch ^ ((r >> 1) & 7))];
-      const int key0 = k0 + 8 * ch;
-      if (key0 < p.N) buf_store16(w, rs, (uint32_t)(((rbase + r) * p.ss2 + key0) * 2));
+      w[i] = stg[base + r * 8 + (ch ^ ((r >> 1) & 7))];
     }
   };
-  // Storer side of split mode: the partner's staged score tile t.
-  auto flush_partner = [&](int t) {
-    if constexpr (kSplit) {
-      if (!loader && p.vec_scores && t >= 0 && t < pwtiles)
-        store_tile(((t & 1) * 4 + pwave) * TSZ, 32 * pwave, t * BN);
+  auto staged_offsets = [&](int rbase, int k0, bool valid, uint32_t (&o)[4])
+                            __attribute__((always_inline)) {
+    const bool ok = valid && k0 + lane_key < p.N;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = ok ? (uint32_t)(((rbase + 8 * i) * ss2 + k0) * 2) + lane_off : kOffNone;
+  };
+  auto zero_store = [&]() __attribute__((always_inline)) {
+    buf_store16(u32x4{0u, 0u, 0u, 0u}, rz, zj.take(lane_off, lane_key, p.N, ss2));
+  };
+  // Score tiles t of the partner (staged by wave pwave in iteration t) and of
+  // the storer itself (staged in iteration t, single buffer).
+  auto staged_pair = [&](int t, u32x4 (&w)[8], uint32_t (&o)[8]) __attribute__((always_inline)) {
+    u32x4 wp[4], wo[4];
+    uint32_t op[4], oo[4];
+    read_staged(((t & 1) * 4 + pwave) * TSZ, wp);
+    read_staged((8 + pwave) * TSZ, wo);
+    staged_offsets(32 * pwave, t * BN, t >= 0 && t < pwtiles, op);
+    staged_offsets(32 * wave, t * BN, t >= 0 && t < wtiles, oo);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w[i] = wp[i];
+      o[i] = op[i];
+      w[4 + i] = wo[i];
+      o[4 + i] = oo[i];
     }
   };
 
@@ -262,137 +309,195 @@ void fwd_kernel(const FwdParams p) {
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = f32x16{};
 
+  // S^T tile: register r of s[kb] holds key k0 + 32*kb + acc_row(r, g).
+  // Every K operand fetch is written before the MFMAs; the caller pins the
+  // schedule (sched_score_tile) so each fetch runs PD k-steps ahead of the
+  // MFMAs that consume it and no MFMA waits on a fresh LDS read.
+  auto score_tile = [&](const uint16_t* kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+    u32x4 a0[KS], a1[KS];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      a0[ks] = lds_row_chunk<D>(kt, perm_row(c), ks, g);
+      a1[ks] = lds_row_chunk<D>(kt, 32 + perm_row(c), ks, g);
+    }
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      s[0] = E::mma(a0[ks], qreg[ks], s[0]);
+      s[1] = E::mma(a1[ks], qreg[ks], s[1]);
+    }
+  };
+  // P = exp2(s*qk_scale - offset), l += rowsum(P), O^T += V^T P^T.
+  auto softmax_pv = [&](const f32x16 (&s)[2], const uint16_t* vt) __attribute__((always_inline)) {
+    const float nb = (m_ref == neg_inf() ? 0.f : m_ref) * p.qk_scale;
+    u32x4 pb[4];
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs) {
+      const f32x16& sv = s[cs >> 1];
+      const int r0 = 8 * (cs & 1);
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        pv[e] = exp2f_fast(fmaf(sv[r0 + e], p.qk_scale, -nb));
+        l_i += pv[e];
+      }
+      pb[cs] = u32x4{E::pack(pv[0], pv[1]), E::pack(pv[2], pv[3]), E::pack(pv[4], pv[5]),
+                     E::pack(pv[6], pv[7])};
+    }
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int cs = 0; cs < 4; ++cs)
+        oacc[db] = E::mma(lds_vt_operand<D>(vt, db, cs, lane), pb[cs], oacc[db]);
+  };
+
   if (ntiles > 0) issue_tile(0, 0);
   if (loader) vm_wait_all();
   lds_barrier();
 
-  for (int it = 0; it < ntiles; ++it) {
-    const int stage = it & 1;
-    if (it + 1 < ntiles) issue_tile(it + 1, stage ^ 1);
-    flush_partner(it - 1);
-    const uint16_t* kt = kv[stage][0];
-    const uint16_t* vt = kv[stage][1];
-    const int k0 = it * BN;
+  // The key-tile loop, instantiated once per wave role so that neither copy
+  // merges with the other inside the loop.
+  auto main_loop = [&](auto role) __attribute__((always_inline)) {
+    constexpr bool ST = decltype(role)::value;
+    for (int it = 0; it < ntiles; ++it) {
+      const int stage = it & 1;
+      if (it + 1 < ntiles) issue_tile(it + 1, stage ^ 1);
+      const uint16_t* kt = kv[stage][0];
+      const uint16_t* vt = kv[stage][1];
+      const int k0 = it * BN;
 
-    if (it < wtiles) {
-      f32x16 s[2] = {f32x16{}, f32x16{}};
+      if (it < wtiles) {
+        f32x16 s[2];
+        if constexpr (ST) {
+          // S = K Q^T with the partner's and its own tile it-1 stored in between.
+          u32x4 w[8];
+          uint32_t o[8];
+          staged_pair(it - 1, w, o);
+          __builtin_amdgcn_sched_barrier(0);
+          score_tile(kt, s);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const u32x4 a0 = lds_row_chunk<D>(kt, perm_row(c), ks, g);
-        const u32x4 a1 = lds_row_chunk<D>(kt, 32 + perm_row(c), ks, g);
-        s[0] = E::mma(a0, qreg[ks], s[0]);
-        s[1] = E::mma(a1, qreg[ks], s[1]);
-      }
-      // Register r of s[kb] holds key k0 + 32*kb + acc_row(r, g).
-      if (it >= tfull) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 32 * kb + acc_row(r, g);
-            const bool ok = key < p.N && (!p.causal || p.causal_off + qrow >= key);
-            if (!ok) s[kb][r] = neg_inf();
-          }
-      }
-
-      if constexpr (MODE == kFwdScores) {
-        if (p.vec_scores) {
-          if (kSplit && loader) {
-            stage_tile((stage * 4 + wave) * TSZ, s, it >= tfull);
-          } else {
-            // A wave reads back its own LDS writes in order: no barrier.
-            const int base = kSplit ? (8 + pwave) * TSZ : wave * TSZ;
-            stage_tile(base, s, it >= tfull);
-            store_tile(base, 32 * wave, k0);
-          }
-        } else if (qrow < p.M) {
-          uint16_t* srow = p.scores + b * p.ss0 + h * p.ss1 + (int64_t)qrow * p.ss2;
+          for (int i = 0; i < 8; ++i) buf_store16(w[i], rs, o[i]);
+          sched_score_tile<KS, 8>();
+        } else {
+          score_tile(kt, s);
+          sched_score_tile<KS, 0>();
+        }
+        if (it >= tfull) {
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = k0 + 32 * kb + acc_row(r, g);
-              const float x = s[kb][r];
-              if (key < p.N) srow[key] = E::cvt(x == neg_inf() ? 0.f : x * p.sm_scale);
+              const bool ok = key < p.N && (!p.causal || p.causal_off + qrow >= key);
+              if (!ok) s[kb][r] = neg_inf();
             }
         }
-      }
-      zero_fill();
-      if constexpr (MODE == kFwdRowSum) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) rsum += s[kb][r] == neg_inf() ? 0.f : s[kb][r];
-      }
-      if constexpr (MODE == kFwdRegion) {
-        if (qrow >= p.split && qrow < p.M && k0 < p.split) {
-          float* brow = p.region + ((int64_t)bh * (p.M - p.split) + (qrow - p.split)) * p.split;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const f32x16& sv = s[j >> 1];
-            const int r0 = 8 * (j & 1);
-            const int key0 = k0 + 16 * j + 8 * g;
-            if (p.vec_region && key0 + 8 <= p.split) {
-              *reinterpret_cast<f32x4*>(brow + key0) =
-                  f32x4{sv[r0 + 0], sv[r0 + 1], sv[r0 + 2], sv[r0 + 3]};
-              *reinterpret_cast<f32x4*>(brow + key0 + 4) =
-                  f32x4{sv[r0 + 4], sv[r0 + 5], sv[r0 + 6], sv[r0 + 7]};
+
+        if constexpr (MODE == kFwdScores) {
+          if (vec) {
+            if (loader) {
+              stage_tile((stage * 4 + wave) * TSZ, s, it >= tfull);
             } else {
+              // A wave reads back its own LDS writes in order: no barrier.
+              stage_tile((8 + pwave) * TSZ, s, it >= tfull);
+            }
+          } else if (qrow < p.M) {
+            uint16_t* srow = p.scores + b * p.ss0 + h * p.ss1 + (int64_t)qrow * p.ss2;
 #pragma unroll
-              for (int e = 0; e < 8; ++e)
-                if (key0 + e < p.split) brow[key0 + e] = sv[r0 + e];
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 32 * kb + acc_row(r, g);
+                const float x = s[kb][r];
+                if (key < p.N) srow[key] = E::cvt(x == neg_inf() ? 0.f : x * p.sm_scale);
+              }
+          }
+        }
+        if constexpr (MODE == kFwdRowSum) {
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) rsum += s[kb][r] == neg_inf() ? 0.f : s[kb][r];
+        }
+        if constexpr (MODE == kFwdRegion) {
+          if (qrow >= p.split && qrow < p.M && k0 < p.split) {
+            float* brow = p.region + ((int64_t)bh * (p.M - p.split) + (qrow - p.split)) * p.split;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const f32x16& sv = s[j >> 1];
+              const int r0 = 8 * (j & 1);
+              const int key0 = k0 + 16 * j + 8 * g;
+              if (p.vec_region && key0 + 8 <= p.split) {
+                *reinterpret_cast<f32x4*>(brow + key0) =
+                    f32x4{sv[r0 + 0], sv[r0 + 1], sv[r0 + 2], sv[r0 + 3]};
+                *reinterpret_cast<f32x4*>(brow + key0 + 4) =
+                    f32x4{sv[r0 + 4], sv[r0 + 5], sv[r0 + 6], sv[r0 + 7]};
+              } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  if (key0 + e < p.split) brow[key0 + e] = sv[r0 + e];
+              }
             }
           }
         }
-      }
 
-      // Online softmax, base 2, on raw scores.
-      float mx = neg_inf();
+        // Online softmax, base 2, on raw scores.
+        float mx = neg_inf();
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const bool grow = mx > m_ref && (m_ref == neg_inf() || (mx - m_ref) * p.qk_scale > 8.f);
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = grow ? mx : m_ref;
-        const float alpha = m_ref == neg_inf() ? 0.f : exp2f_fast((m_ref - m_new) * p.qk_scale);
-        l_i *= alpha;
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const bool grow = mx > m_ref && (m_ref == neg_inf() || (mx - m_ref) * p.qk_scale > 8.f);
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float m_new = grow ? mx : m_ref;
+          const float alpha = m_ref == neg_inf() ? 0.f : exp2f_fast((m_ref - m_new) * p.qk_scale);
+          l_i *= alpha;
 #pragma unroll
-        for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
-        m_ref = m_new;
-      }
-      const float nb = (m_ref == neg_inf() ? 0.f : m_ref) * p.qk_scale;
-      u32x4 pb[4];
-#pragma unroll
-      for (int cs = 0; cs < 4; ++cs) {
-        const f32x16& sv = s[cs >> 1];
-        const int r0 = 8 * (cs & 1);
-        float pv[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          pv[e] = exp2f_fast(fmaf(sv[r0 + e], p.qk_scale, -nb));
-          l_i += pv[e];
+          for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+          m_ref = m_new;
         }
-        pb[cs] = u32x4{E::pack(pv[0], pv[1]), E::pack(pv[2], pv[3]), E::pack(pv[4], pv[5]),
-                       E::pack(pv[6], pv[7])};
+        if constexpr (ST) {
+          // O += P V with zero slots in between.
+          softmax_pv(s, vt);
+#pragma unroll
+          for (int z = 0; z < kZero; ++z) zero_store();
+          interleave_mfma_stores<kZero>();
+        } else {
+          softmax_pv(s, vt);
+        }
+      } else if constexpr (ST) {
+        u32x4 w[8];
+        uint32_t o[8];
+        staged_pair(it - 1, w, o);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) buf_store16(w[i], rs, o[i]);
+#pragma unroll
+        for (int z = 0; z < kZero; ++z) zero_store();
       }
-#pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int cs = 0; cs < 4; ++cs)
-          oacc[db] = E::mma(lds_vt_operand<D>(vt, db, cs, lane), pb[cs], oacc[db]);
-    } else {
-      zero_fill();
+      if (loader) vm_wait_all();
+      lds_barrier();
     }
-    if (loader) vm_wait_all();
-    lds_barrier();
+  };
+  if constexpr (kSplit) {
+    if (storer)
+      main_loop(std::true_type{});
+    else
+      main_loop(std::false_type{});
+  } else {
+    main_loop(std::false_type{});
   }
-  flush_partner(ntiles - 1);
   if constexpr (MODE == kFwdScores) {
-    zf_own.run(32, rz, p.ss2);
-    if constexpr (kSplit) zf_partner.run(32, rz, p.ss2);
-    if (!p.vec_scores) {  // element-wise zero triangle for unaligned rows
+    if (storer) {
+      u32x4 w[8];
+      uint32_t o[8];
+      staged_pair(ntiles - 1, w, o);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) buf_store16(w[i], rs, o[i]);
+      while (zj.pending()) zero_store();
+    }
+    if (!vec) {  // element-wise zero triangle for unaligned rows
       const int z0 = min(p.N, wtiles * BN);
       for (int rr = 0; rr < 32; ++rr) {
         const int row = wrow0 + rr;

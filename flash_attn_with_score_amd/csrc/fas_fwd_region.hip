@@ -3,8 +3,7 @@
 
 namespace fas {
 
-hipError_t launch_fwd_region(const FwdParams& p, int dtype, int d, int waves, hipStream_t s) {
-  (void)waves;
+hipError_t launch_fwd_region(const FwdParams& p, int dtype, int d, hipStream_t s) {
   return launch_fwd_mode<kFwdRegion, 8>(p, dtype, d, s);
 }
 

@@ -9,10 +9,9 @@
 namespace fas {
 
 // Forward pass (fas_fwd.hpp); mode is a FwdMode, dtype 0 = fp16, 1 = bf16.
-// waves selects 4 or 8 wave64s per workgroup (head dim 128 only).
-hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, int waves, hipStream_t s);
-// Rows per workgroup of launch_fwd for (d, waves).
-int fwd_rows_per_block(int d, int waves);
+hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, hipStream_t s);
+// Query rows per forward workgroup (8 wave64s x 32 rows).
+constexpr int kFwdRows = 256;
 
 // Softmax-weight column sums after a forward pass that wrote lse2.
 hipError_t launch_colsm(const ColsmParams& p, int dtype, int d, bool buffered, hipStream_t s);
