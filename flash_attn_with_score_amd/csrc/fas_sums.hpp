@@ -76,6 +76,12 @@ void colsm_kernel(const ColsmParams p) {
     for (int ks = 0; ks < KS; ++ks)
       kreg[kblk][ks] =
           buf_load16(rk, (uint32_t)(((key0 + 32 * kblk + c) * p.sk2 + 16 * ks + 8 * g) * 2));
+  // Settle the K loads here: left pending, the compiler's wait counters for
+  // them would also hold back (vmcnt N) on the Q prefetch inside the loop.
+#pragma unroll
+  for (int kblk = 0; kblk < 2; ++kblk)
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[kblk][ks]));
 
   // Query tiles that can see any key of the workgroup.
   int rstart = p.row_lo;
@@ -90,7 +96,7 @@ void colsm_kernel(const ColsmParams p) {
     for (int i = 0; i < CPT; ++i) {
       const int id = tid + i * NT;
       const int row = id / CPR, ch = id % CPR;
-      qst[i] = buf_load16(rq, (uint32_t)(((t * TQ + row) * p.sq2 + ch * 8) * 2)) ^ p.qneg;
+      qst[i] = buf_load16(rq, (uint32_t)(((t * TQ + row) * p.sq2 + ch * 8) * 2));
     }
     if (tid < TQ) {
       const int row = t * TQ + tid;
@@ -103,7 +109,9 @@ void colsm_kernel(const ColsmParams p) {
       const int id = tid + i * NT;
       if (CHUNKS % NT == 0 || id < CHUNKS) {
         const int row = id / CPR, ch = id % CPR;
-        *reinterpret_cast<u32x4*>(&qlds[stage][tile_off<D>(row, ch)]) = qst[i];
+        // The sign flip is applied here, after the tile's compute, so the
+        // prefetch loads are not waited for at the top of the iteration.
+        *reinterpret_cast<u32x4*>(&qlds[stage][tile_off<D>(row, ch)]) = qst[i] ^ p.qneg;
       }
     }
     if (tid < TQ) llds[stage][tid] = lst;
