@@ -6,8 +6,9 @@ namespace fas {
 
 template <class E, int D>
 static hipError_t colsm_t(const ColsmParams& p, hipStream_t s) {
-  const dim3 grid((unsigned)((int64_t)p.nkb * p.B * p.H));
-  hipLaunchKernelGGL((colsm_kernel<E, D>), grid, dim3(256), 0, s, p);
+  // One workgroup per mirror pair of key blocks.
+  const dim3 grid((unsigned)((int64_t)((p.nkb + 1) / 2) * p.B * p.H));
+  hipLaunchKernelGGL((colsm_kernel<E, D>), grid, dim3(512), 0, s, p);
   return hipGetLastError();
 }
 

@@ -2,9 +2,9 @@
 //
 // Softmax-weight column sums (attention_with_col_softmax_sum.py:195-270,
 // attention_cross_token_softmax_sum.py:203-268 and the buffered :568-627)
-// are computed after the forward pass, key-block outer: a workgroup owns 256
-// keys of one (batch, query head), keeps them in VGPRs and streams the query
-// rows that can see them.  S = Q K^T puts keys on lanes and queries in the
+// are computed after the forward pass, key-block outer: a workgroup owns two
+// blocks of 256 keys of one (batch, query head), keeps them in VGPRs and
+// streams the query rows that can see them.  S = Q K^T puts keys on lanes and queries in the
 // accumulator registers, so P = exp2(s*qk_scale - lse2[row]) (the forward
 // pass's final base-2 log-sum-exp) is summed over queries in-lane.  Every
 // column is owned by one workgroup: no atomics, the result is deterministic.
@@ -41,13 +41,18 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
   }
 }
 
+// Key blocks of 256 are dealt in mirror pairs (pb, nkb-1-pb): under a causal
+// mask block kb sees (M - 256 kb) query rows, so a pair always sums to the
+// same amount of work and every workgroup finishes together.  Each of the 8
+// waves owns 32 keys of each block of the pair; both groups share the
+// A operand (the Q chunk) of S = Q K^T, and the later block's MFMAs start
+// only on the query tiles that can see it.
 template <class E, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void colsm_kernel(const ColsmParams p) {
   constexpr int KS = D / 16;
-  constexpr int NT = 256;
-  constexpr int KW = 64;            // keys per wave
-  constexpr int BK = 4 * KW;        // keys per workgroup
+  constexpr int NT = 512;
+  constexpr int BK = 256;           // keys per block (8 waves x 32)
   constexpr int TQ = 64;            // query rows per tile
   constexpr int CPR = D / 8;
   constexpr int CHUNKS = TQ * CPR;
@@ -59,33 +64,37 @@ void colsm_kernel(const ColsmParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
-  int kb, bh;
-  map_block_keys(blockIdx.x, p.nkb, p.B * p.H, kb, bh);
+  const int npairs = (p.nkb + 1) / 2;
+  int pb, bh;
+  map_block_keys(blockIdx.x, npairs, p.B * p.H, pb, bh);
   const int h = bh % p.H, b = bh / p.H, hk = h / p.G;
-  const int key0 = kb * BK + KW * wave;
+  const int kbb = p.nkb - 1 - pb;
+  const bool has_b = kbb != pb;
+  // Keys of this wave: group 0 [key0[0], +32) in block pb, group 1 in kbb.
+  const int key0[2] = {pb * BK + 32 * wave, kbb * BK + 32 * wave};
 
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
   const float* lse = p.lse2 + (int64_t)bh * p.M;
 
-  // K (B operand of S = Q K^T): lane holds K[key0 + 32*kblk + c][16ks + 8g, +8).
+  // K (B operand of S = Q K^T): lane holds K[key0[grp] + c][16ks + 8g, +8).
   u32x4 kreg[2][KS];
 #pragma unroll
-  for (int kblk = 0; kblk < 2; ++kblk)
+  for (int grp = 0; grp < 2; ++grp)
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
-      kreg[kblk][ks] =
-          buf_load16(rk, (uint32_t)(((key0 + 32 * kblk + c) * p.sk2 + 16 * ks + 8 * g) * 2));
+      kreg[grp][ks] =
+          buf_load16(rk, (uint32_t)(((key0[grp] + c) * p.sk2 + 16 * ks + 8 * g) * 2));
   // Settle the K loads here: left pending, the compiler's wait counters for
   // them would also hold back (vmcnt N) on the Q prefetch inside the loop.
 #pragma unroll
-  for (int kblk = 0; kblk < 2; ++kblk)
+  for (int grp = 0; grp < 2; ++grp)
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[kblk][ks]));
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[grp][ks]));
 
-  // Query tiles that can see any key of the workgroup.
+  // Query tiles that can see any key of block pb (a superset of kbb's).
   int rstart = p.row_lo;
-  if (p.causal) rstart = max(rstart, kb * BK - p.causal_off);
+  if (p.causal) rstart = max(rstart, pb * BK - p.causal_off);
   const int t0 = max(0, rstart) / TQ;
   const int t1 = (p.M + TQ - 1) / TQ;
 
@@ -128,24 +137,44 @@ void colsm_kernel(const ColsmParams p) {
     const bool more = t + 1 < t1;
     if (more) fetch(t + 1);
     const int r0 = t * TQ;
-    bool live = true, full = true;
+    // Group grp is live if some row of the tile sees its first key, full if
+    // every row sees its last key.
+    bool live[2] = {true, has_b}, full[2] = {true, true};
     if (p.causal) {
-      live = p.causal_off + r0 + TQ - 1 >= key0;
-      full = p.causal_off + r0 >= key0 + KW - 1;
+#pragma unroll
+      for (int grp = 0; grp < 2; ++grp) {
+        live[grp] = live[grp] && p.causal_off + r0 + TQ - 1 >= key0[grp];
+        full[grp] = p.causal_off + r0 >= key0[grp] + 31;
+      }
     }
-    // Both query blocks of the tile; the causal mask only on diagonal tiles
-    // (separate code, so full tiles carry no per-element test).
-    auto body = [&](auto mask_tag) __attribute__((always_inline)) {
+    // Both query blocks of the tile for group 0 and, when TWO, group 1; the
+    // causal mask only where a group crosses the diagonal (separate code, so
+    // full tiles carry no per-element test).
+    auto body = [&](auto two_tag, auto mask_tag) __attribute__((always_inline)) {
+      constexpr bool TWO = decltype(two_tag)::value;
       constexpr bool MASK = decltype(mask_tag)::value;
+      constexpr int NG = TWO ? 2 : 1;
       const uint16_t* qt = qlds[stage];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
+        // Operand fetches run two k-steps ahead of their MFMAs (pinned
+        // schedule), so no MFMA waits on a fresh LDS read.
+        u32x4 a[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a[ks] = lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g);
         f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const u32x4 a = lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g);
-          s[0] = E::mma(a, kreg[0][ks], s[0]);
-          s[1] = E::mma(a, kreg[1][ks], s[1]);
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+          for (int grp = 0; grp < NG; ++grp) s[grp] = E::mma(a[ks], kreg[grp][ks], s[grp]);
+        {
+          constexpr int PD = KS < 2 ? KS : 2;
+          __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);  // DS read
+#pragma unroll
+          for (int i = 0; i < KS; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, NG, 0);  // MFMA
+            if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          }
         }
         // Register r holds query row r0 + 32qb + acc_row(r, g).
         float lr[16];
@@ -158,36 +187,42 @@ void colsm_kernel(const ColsmParams p) {
           lr[8 * hf + 4] = x1.x; lr[8 * hf + 5] = x1.y; lr[8 * hf + 6] = x1.z; lr[8 * hf + 7] = x1.w;
         }
 #pragma unroll
-        for (int kblk = 0; kblk < 2; ++kblk) {
+        for (int grp = 0; grp < NG; ++grp) {
           float pr[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            pr[r] = exp2f_fast(fmaf(s[kblk][r], p.qk_scale, -lr[r]));
+            pr[r] = exp2f_fast(fmaf(s[grp][r], p.qk_scale, -lr[r]));
             if constexpr (MASK) {
               const int row = r0 + 32 * qb + acc_row(r, g);
-              if (p.causal_off + row < key0 + 32 * kblk + c) pr[r] = 0.f;
+              if (p.causal_off + row < key0[grp] + c) pr[r] = 0.f;
             }
           }
 #pragma unroll
           for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
             for (int r = 0; r < w; ++r) pr[r] += pr[r + w];
-          colacc[kblk] += pr[0];
+          colacc[grp] += pr[0];
         }
       }
     };
-    if (live) {
-      if (full) body(std::false_type{});
-      else body(std::true_type{});
+    if (live[0]) {
+      if (live[1]) {
+        if (full[0] && full[1]) body(std::true_type{}, std::false_type{});
+        else body(std::true_type{}, std::true_type{});
+      } else {
+        if (full[0]) body(std::false_type{}, std::false_type{});
+        else body(std::false_type{}, std::true_type{});
+      }
     }
     if (more) stash(stage ^ 1);
     __syncthreads();
   }
 #pragma unroll
-  for (int kblk = 0; kblk < 2; ++kblk) {
-    const float tot = colacc[kblk] + __shfl_xor(colacc[kblk], 32);
-    const int key = key0 + 32 * kblk + c;
-    if (g == 0 && key < p.ncols) p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot;
+  for (int grp = 0; grp < 2; ++grp) {
+    const float tot = colacc[grp] + __shfl_xor(colacc[grp], 32);
+    const int key = key0[grp] + c;
+    if (g == 0 && (grp == 0 || has_b) && key < p.ncols)
+      p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot;
   }
 }
 
