@@ -372,8 +372,11 @@ void fwd_kernel(const FwdParams p) {
   // merges with the other inside the loop.
   auto main_loop = [&](auto role) __attribute__((always_inline)) {
     constexpr bool ST = decltype(role)::value;
-    for (int it = 0; it < ntiles; ++it) {
-      const int stage = it & 1;
+    // One key tile; the LDS stage is a compile-time constant, so the
+    // per-lane operand addresses are loop-invariant and the stage offset
+    // folds into the LDS instructions' immediate offsets.
+    auto step = [&](int it, auto stage_tag) __attribute__((always_inline)) {
+      constexpr int stage = decltype(stage_tag)::value;
       if (it + 1 < ntiles) issue_tile(it + 1, stage ^ 1);
       const uint16_t* kt = kv[stage][0];
       const uint16_t* vt = kv[stage][1];
@@ -490,6 +493,10 @@ void fwd_kernel(const FwdParams p) {
       }
       if (loader) vm_wait_all();
       lds_barrier();
+    };
+    for (int it = 0; it < ntiles; it += 2) {
+      step(it, std::integral_constant<int, 0>{});
+      if (it + 1 < ntiles) step(it + 1, std::integral_constant<int, 1>{});
     }
   };
   if constexpr (kSplit) {
