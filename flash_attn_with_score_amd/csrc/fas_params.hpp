@@ -69,7 +69,7 @@ struct ColsmParams {
 struct RawParams {
   const uint16_t* q;
   const uint16_t* k;
-  float* bsum;           // (B*Hk, nblk + 1, D) fp32 block sums -> exclusive suffix sums
+  float* bsum;           // (B*Hk, nblk + 1, D) fp32 per-block sums of q (slot nblk unused)
   float* out;            // (B, Hk, ncols) strided
   int64_t sq0, sq1, sq2;
   int64_t sk0, sk1, sk2;

@@ -52,7 +52,6 @@ static hipError_t rawsum_t(const RawParams& p, bool suffix, hipStream_t s) {
   const unsigned bhk = (unsigned)(p.B * p.Hk);
   if (p.nblk > 0)
     hipLaunchKernelGGL((qsum_blocks_kernel<E, D>), dim3((unsigned)p.nblk, bhk), dim3(256), 0, s, p);
-  hipLaunchKernelGGL(suffix_blocks_kernel, dim3(bhk), dim3(D < 64 ? 64 : D), 0, s, p);
   if (suffix) {
     const unsigned nw = (unsigned)((p.M + 63) / 64 + p.nextra);
     if (nw > 0) hipLaunchKernelGGL((colraw_kernel<E, D, true>), dim3(nw, bhk), dim3(256), 0, s, p);

@@ -14,10 +14,10 @@
 // attention_with_col_sum_sequential.py:177-182,
 // attention_cross_token_qk_sum.py:169-216) are linear in q:
 //   sum_{i admissible for j} (q_i . k_j) * sm_scale = (sum_i q_i) . k_j * sm_scale
-// so they need per-64-row block sums of q (qsum_blocks_kernel), their
-// exclusive suffix sums (suffix_blocks_kernel) and one dot product per key
-// (colraw_kernel): O(N*D) work and one read of Q and K instead of a
-// reduction over the N*N score matrix.
+// so they need per-64-row block sums of q (qsum_blocks_kernel) and one dot
+// product per key (colraw_kernel, which also forms the exclusive suffix over
+// blocks and the in-block suffix): O(N*D) work and one read of Q and K
+// instead of a reduction over the N*N score matrix.
 #pragma once
 #include "fas_device.hpp"
 #include "fas_params.hpp"
@@ -317,19 +317,31 @@ __global__ __launch_bounds__(256) void qsum_blocks_kernel(const RawParams p) {
   }
 }
 
-// In place: bsum[blk] <- sum of blocks after blk; bsum[nblk] <- total.
-__global__ void suffix_blocks_kernel(const RawParams p) {
-  const int bhk = blockIdx.x;
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
-    float* col = p.bsum + (int64_t)bhk * (p.nblk + 1) * p.D + d;
-    float acc = 0.f;
-    for (int blk = p.nblk - 1; blk >= 0; --blk) {
-      const float t = col[(int64_t)blk * p.D];
-      col[(int64_t)blk * p.D] = acc;
-      acc += t;
-    }
-    col[(int64_t)p.nblk * p.D] = acc;
+// out[d] = sum of the block sums bs[blk][d] for blk in [lo, hi), by all 256
+// threads of the workgroup (256/D per dimension, blocks strided between
+// them, then a fixed-order combine), so the loads are independent and in
+// flight together.  Call from every thread; ends with a barrier.
+template <int D>
+__device__ __forceinline__ void block_range_sum(const float* bs, int lo, int hi, float* out,
+                                                float* scratch) {
+  constexpr int TP = 256 / D;
+  const int d = threadIdx.x % D, part = threadIdx.x / D;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  int blk = lo + part;
+  for (; blk + 3 * TP < hi; blk += 4 * TP) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] += bs[(int64_t)(blk + u * TP) * D + d];
   }
+  for (; blk < hi; blk += TP) acc[0] += bs[(int64_t)blk * D + d];
+  scratch[threadIdx.x] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (part == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < TP; ++j) t += scratch[d + j * D];
+    out[d] = t;
+  }
+  __syncthreads();
 }
 
 // One dot product per key with a per-key fp32 vector held in LDS rows.
@@ -364,6 +376,8 @@ __device__ __forceinline__ float key_dot(const RawParams& p, const uint16_t* kba
 template <class E, int D, bool SUFFIX>
 __global__ __launch_bounds__(256) void colraw_kernel(const RawParams p) {
   __shared__ float vec[64][D];
+  __shared__ float seed[D];
+  __shared__ float scratch[256];
   const int bhk = blockIdx.y;
   const int hk = bhk % p.Hk, b = bhk / p.Hk;
   const float* bs = p.bsum + (int64_t)bhk * (p.nblk + 1) * D;
@@ -372,8 +386,8 @@ __global__ __launch_bounds__(256) void colraw_kernel(const RawParams p) {
   const int kslot = threadIdx.x >> 2, part = threadIdx.x & 3;
 
   if (!SUFFIX || w < p.nextra) {
-    for (int d = threadIdx.x; d < D; d += 256) vec[0][d] = bs[(int64_t)p.nblk * D + d];
-    __syncthreads();
+    // Keys every query row sees: the sum over all row blocks.
+    block_range_sum<D>(bs, 0, p.nblk, vec[0], scratch);
     const int key = 64 * w + kslot;
     const int lim = SUFFIX ? min(p.ncols, p.causal_off) : p.ncols;
     if (key < lim) {
@@ -385,6 +399,8 @@ __global__ __launch_bounds__(256) void colraw_kernel(const RawParams p) {
   // In-block suffix sums over rows [64rb, 64rb + 64) of the group's heads.
   const int rb = w - p.nextra;
   const int r0 = 64 * rb;
+  // Rows of the later row blocks: the exclusive suffix over blocks.
+  block_range_sum<D>(bs, rb + 1, p.nblk, seed, scratch);
   for (int i = threadIdx.x; i < 64 * D; i += 256) (&vec[0][0])[i] = 0.f;
   __syncthreads();
   {
@@ -404,11 +420,22 @@ __global__ __launch_bounds__(256) void colraw_kernel(const RawParams p) {
     }
   }
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += 256) {
-    float acc = bs[(int64_t)rb * D + d];
-    for (int rr = 63; rr >= 0; --rr) {
-      acc += vec[rr][d];
-      vec[rr][d] = acc;
+  {
+    // In-block suffix scan, 256/D threads per dimension: each scans a
+    // segment of 64*D/256 rows seeded with the later segments' totals.
+    constexpr int TP = 256 / D, SEG = 64 / TP;
+    const int d = threadIdx.x % D, part = threadIdx.x / D;
+    float tot = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < SEG; ++rr) tot += vec[part * SEG + rr][d];
+    scratch[threadIdx.x] = tot;
+    __syncthreads();
+    float acc = seed[d];
+    for (int j = TP - 1; j > part; --j) acc += scratch[d + j * D];
+#pragma unroll
+    for (int rr = SEG - 1; rr >= 0; --rr) {
+      acc += vec[part * SEG + rr][d];
+      vec[part * SEG + rr][d] = acc;
     }
   }
   __syncthreads();
