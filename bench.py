@@ -13,6 +13,12 @@ resident in HBM.  The line printed is the driver's JSON contract plus
   secondary     the softmax column-sum kernel at the same shape against the
                 fp16 MFMA peak.
 
+The default warmup (300 steps, about 70 ms) is sized for the GPU's clock
+ramp: from idle, the first ~25 ms of calls run up to 30% slower while the
+clocks rise (measured on the MI355X: 302 us per scores call in the first
+5 ms, 231 us from ~25 ms on, at the 1400 W board power limit).  Timing fewer
+warmup steps measures the ramp, not the kernel.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
 from __future__ import annotations
@@ -192,8 +198,8 @@ def time_steps(call, steps: int, warmup: int):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="scores")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--heads", type=int, default=32)

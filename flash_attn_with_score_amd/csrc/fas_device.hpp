@@ -120,6 +120,11 @@ __device__ __forceinline__ void buf_store16(u32x4 v, __amdgpu_buffer_rsrc_t r, u
 __device__ __forceinline__ void buf_store16_nt(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off) {
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kAuxNT);
 }
+// The same with a wave-uniform scalar byte offset soff added to off.
+__device__ __forceinline__ void buf_store16_nt(u32x4 v, __amdgpu_buffer_rsrc_t r, uint32_t off,
+                                               uint32_t soff) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, soff, kAuxNT);
+}
 
 // Row permutation applied to MFMA operand rows (bits 2 and 3 swapped).  With
 // it the 16 accumulator registers of lane l (g = l / 32) cover rows

@@ -78,42 +78,74 @@ constexpr uint32_t kOffNone = 0x80000000u;
 
 // Zero writer for the never-computed causal part of two 32-row rectangles of
 // a row block: rows [ra, ra + 32) x keys [za, N) and rows [rb, rb + 32) x
-// keys [zb, N) (row numbers relative to the block).  Each store covers 8 rows
-// x 64 keys: eight full 128-byte row segments, lane l writing row l / 8,
-// 16-byte chunk l % 8.  Stores walk each 8-row group's keys left to right
-// before moving to the next group, so the HBM sees long runs along each row:
+// keys [zb, N) (row numbers relative to the block, za and zb multiples of
+// 64).  Each store covers 8 rows x 64 keys: eight full 128-byte row
+// segments, lane l writing row l / 8, 16-byte chunk l % 8.  The writer walks
+// eight runs -- the 8-row groups of a, then those of b -- each left to right
+// in batches of eight 64-key blocks, so the HBM sees long runs along each row:
 // measured on the MI355X, writing a 1 GiB score matrix this way runs at
-// 6.2 TB/s against 3.9 TB/s when every store moves to other rows.  Every
-// store is computed from wave-uniform values plus one lane constant.
-struct ZeroJob {
-  int na = 0, nb = 0, next = 0;      // stores in rectangle a, b; stores taken
-  int ra = 0, rb = 0, za = 0, zb = 0;
-  int kba = 0, kbb = 0;              // 64-key blocks per row in a, b
-  int rg = 0, kb = 0;                // position in the current rectangle
+// 6.2 TB/s against 3.9 TB/s when every store moves to other rows.
+// Inside the key loop only full batches are written: eight blocks that lie
+// wholly below key N.  Store i of a batch takes the lane's row offset as
+// voffset (rows past the block's extent fall outside the buffer and are
+// dropped), the batch's key offset as the wave-uniform scalar offset and
+// 128*i as the immediate, so a batch costs one vector select and scalar
+// bookkeeping.  The remaining blocks of each run (fewer than eight, the last
+// one possibly cut by N) are written by tail() after the loop.
+struct ZeroRuns {
+  int run = 8;          // current run, 0-3 in a, 4-7 in b, 8 = no full batch left
+  int nb = 0;           // full batches left in the current run
+  uint32_t koff = 0;    // byte offset of the batch's first key
+  uint32_t roff = 0;    // byte offset of the run's first row
+  int ra = 0, rb = 0, za = 0, zb = 0, ca = 0, cb = 0, N = 0;
+  uint32_t row_bytes = 0;
 
+  // 64-key blocks per row of a rectangle starting at key z with rows_valid
+  // rows inside the matrix, and how many full batches they hold.
   __device__ __forceinline__ static int blocks(int N, int z, int rows_valid) {
     return (rows_valid > 0 && N > z) ? (N - z + 63) >> 6 : 0;
   }
-  __device__ __forceinline__ void set(int ra_, int za_, int kba_, int rb_, int zb_, int kbb_) {
-    ra = ra_; za = za_; kba = kba_; na = 4 * kba_;
-    rb = rb_; zb = zb_; kbb = kbb_; nb = 4 * kbb_;
+  __device__ __forceinline__ static int full_batches(int N, int c) {
+    return c > 0 ? (c - ((N & 63) != 0 ? 1 : 0)) >> 3 : 0;
   }
-  __device__ __forceinline__ bool pending() const { return next < na + nb; }
-  // Byte offset of this lane's 16 bytes in store `next` (kOffNone when past
-  // the end of the job or past key N - 1), then advance.
-  __device__ __forceinline__ uint32_t take(uint32_t lane_off, int lane_key, int N, int ss2) {
-    const int s = next++;
-    const bool in_a = s < na;
-    const int r = (in_a ? ra : rb) + 8 * rg;
-    const int k = (in_a ? za : zb) + 64 * kb;
-    const bool ok = s < na + nb && k + lane_key < N;
-    // Next position: key block first, then row group; rectangle a holds
-    // exactly 4 x kba stores, so b starts at (0, 0).
-    if (++kb == (in_a ? kba : kbb)) {
-      kb = 0;
-      rg = (rg + 1) & 3;
+  __device__ __forceinline__ void init(int ra_, int za_, int rows_a, int rb_, int zb_, int rows_b,
+                                       int N_, int ss2) {
+    ra = ra_; rb = rb_; za = za_; zb = zb_; N = N_;
+    row_bytes = (uint32_t)ss2 * 2u;
+    ca = blocks(N, za, rows_a);
+    cb = blocks(N, zb, rows_b);
+    start(full_batches(N, ca) > 0 ? 0 : (full_batches(N, cb) > 0 ? 4 : 8));
+  }
+  __device__ __forceinline__ void start(int r) {
+    run = r;
+    const bool in_a = r < 4;
+    nb = r < 8 ? full_batches(N, in_a ? ca : cb) : 0;
+    koff = (uint32_t)(in_a ? za : zb) * 2u;
+    roff = (uint32_t)((in_a ? ra : rb) + 8 * (r & 3)) * row_bytes;
+  }
+  __device__ __forceinline__ bool pending() const { return run < 8; }
+  // voffset of store 0 of the current batch (kOffNone once no full batch is
+  // left); store i adds 128*i.
+  __device__ __forceinline__ uint32_t vbase(uint32_t lane_off) const {
+    return run < 8 ? lane_off + roff : kOffNone;
+  }
+  __device__ __forceinline__ void advance() {
+    koff += 1024u;
+    if (--nb == 0 && run < 8)
+      start(run == 3 && full_batches(N, cb) == 0 ? 8 : run + 1);
+  }
+  // Blocks of every run past its full batches, masked at key N.
+  template <class Store>
+  __device__ __forceinline__ void tail(uint32_t lane_off, int lane_key, Store&& store) const {
+    for (int r = 0; r < 8; ++r) {
+      const bool in_a = r < 4;
+      const int c = in_a ? ca : cb, z = in_a ? za : zb;
+      const uint32_t ro = (uint32_t)((in_a ? ra : rb) + 8 * (r & 3)) * row_bytes;
+      for (int kb = 8 * full_batches(N, c); kb < c; ++kb) {
+        const int k = z + 64 * kb;
+        store(lane_key < N - k ? lane_off + ro : kOffNone, (uint32_t)k * 2u);
+      }
     }
-    return ok ? (uint32_t)((r * ss2 + k) * 2) + lane_off : kOffNone;
   }
 };
 
@@ -166,7 +198,7 @@ void fwd_kernel(const FwdParams p) {
   constexpr int TSZ = 256;  // 16-byte units per wave tile
   constexpr int SG = kSplit ? (8 + 4) * TSZ : 1;
   // Zero-store slots per key tile and storer (issued during O += P V).
-  constexpr int kZero = 8;
+  constexpr int kZero = 8;  // zero stores per key tile: one ZeroRuns batch
 
   __shared__ __attribute__((aligned(16))) uint16_t kv[2][2][TILE];
   __shared__ __attribute__((aligned(16))) u32x4 stg[SG];
@@ -238,7 +270,7 @@ void fwd_kernel(const FwdParams p) {
   const uint32_t lane_off = (uint32_t)(((lane >> 3) * ss2 + lane_key) * 2);
   __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scores, 0);
   __amdgpu_buffer_rsrc_t rz = rs;
-  ZeroJob zj;
+  ZeroRuns zr;
   if constexpr (MODE == kFwdScores) {
     const int64_t base = b * p.ss0 + h * p.ss1 + (int64_t)row0 * p.ss2;
     const int rows = max(0, min(BM, p.M - row0));
@@ -252,8 +284,8 @@ void fwd_kernel(const FwdParams p) {
                    __builtin_amdgcn_readfirstlane((uint32_t)(mrows * p.ss2 * 2)));
     if (storer) {
       const int wa = wtiles_of(mrow0 + 32 * wave), wb = wtiles_of(mrow0 + 32 * pwave);
-      zj.set(32 * wave, wa * BN, ZeroJob::blocks(p.N, wa * BN, p.M - (mrow0 + 32 * wave)),
-             32 * pwave, wb * BN, ZeroJob::blocks(p.N, wb * BN, p.M - (mrow0 + 32 * pwave)));
+      zr.init(32 * wave, wa * BN, p.M - (mrow0 + 32 * wave), 32 * pwave, wb * BN,
+              p.M - (mrow0 + 32 * pwave), p.N, ss2);
     }
   }
   // Staged score tile: row r (32 rows), 16-byte chunk ch (8 per row) at
@@ -295,8 +327,13 @@ void fwd_kernel(const FwdParams p) {
     for (int i = 0; i < 4; ++i)
       o[i] = ok ? (uint32_t)(((rbase + 8 * i) * ss2 + k0) * 2) + lane_off : kOffNone;
   };
-  auto zero_store = [&]() __attribute__((always_inline)) {
-    buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rz, zj.take(lane_off, lane_key, p.N, ss2));
+  // One batch of kZero = 8 zero stores.
+  auto zero_batch = [&]() __attribute__((always_inline)) {
+    const uint32_t vb = zr.vbase(lane_off);
+#pragma unroll
+    for (int i = 0; i < kZero; ++i)
+      buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rz, vb + 128u * (uint32_t)i, zr.koff);
+    zr.advance();
   };
   // Score tiles t of the partner (staged by wave pwave in iteration t) and of
   // the storer itself (staged in iteration t, single buffer).
@@ -374,9 +411,13 @@ void fwd_kernel(const FwdParams p) {
     constexpr bool ST = decltype(role)::value;
     // One key tile; the LDS stage is a compile-time constant, so the
     // per-lane operand addresses are loop-invariant and the stage offset
-    // folds into the LDS instructions' immediate offsets.
-    auto step = [&](int it, auto stage_tag) __attribute__((always_inline)) {
+    // folds into the LDS instructions' immediate offsets. Only the copy
+    // with MK set carries the causal / key-range mask, so tiles below the
+    // diagonal run no compare-and-select code at all.
+    auto step = [&](int it, auto stage_tag, auto mask_tag) __attribute__((always_inline)) {
       constexpr int stage = decltype(stage_tag)::value;
+      constexpr bool MK = decltype(mask_tag)::value;
+      const bool masked = MK && it >= tfull;
       if (it + 1 < ntiles) issue_tile(it + 1, stage ^ 1);
       const uint16_t* kt = kv[stage][0];
       const uint16_t* vt = kv[stage][1];
@@ -398,7 +439,7 @@ void fwd_kernel(const FwdParams p) {
           score_tile(kt, s);
           sched_score_tile<KS, 0>();
         }
-        if (it >= tfull) {
+        if (masked) {
 #pragma unroll
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -412,10 +453,10 @@ void fwd_kernel(const FwdParams p) {
         if constexpr (MODE == kFwdScores) {
           if (vec) {
             if (loader) {
-              stage_tile((stage * 4 + wave) * TSZ, s, it >= tfull);
+              stage_tile((stage * 4 + wave) * TSZ, s, masked);
             } else {
               // A wave reads back its own LDS writes in order: no barrier.
-              stage_tile((8 + pwave) * TSZ, s, it >= tfull);
+              stage_tile((8 + pwave) * TSZ, s, masked);
             }
           } else if (qrow < p.M) {
             uint16_t* srow = p.scores + b * p.ss0 + h * p.ss1 + (int64_t)qrow * p.ss2;
@@ -476,8 +517,7 @@ void fwd_kernel(const FwdParams p) {
         if constexpr (ST) {
           // O += P V with zero slots in between.
           softmax_pv(s, vt);
-#pragma unroll
-          for (int z = 0; z < kZero; ++z) zero_store();
+          zero_batch();
           interleave_mfma_stores<kZero>();
         } else {
           softmax_pv(s, vt);
@@ -488,15 +528,25 @@ void fwd_kernel(const FwdParams p) {
         staged_pair(it - 1, w, o);
 #pragma unroll
         for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
-#pragma unroll
-        for (int z = 0; z < kZero; ++z) zero_store();
+        zero_batch();
       }
       if (loader) vm_wait_all();
       lds_barrier();
     };
-    for (int it = 0; it < ntiles; it += 2) {
-      step(it, std::integral_constant<int, 0>{});
-      if (it + 1 < ntiles) step(it + 1, std::integral_constant<int, 1>{});
+    // Tile it uses LDS stage it & 1. Pairs of full tiles first, then the
+    // rest (diagonal and key-edge tiles, and an odd full tile) masked; every
+    // wave runs ntiles steps in all, one workgroup barrier each.
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    const int tpairs = min(tfull, ntiles) & ~1;
+    int it = 0;
+    for (; it < tpairs; it += 2) {
+      step(it, S0{}, std::false_type{});
+      step(it + 1, S1{}, std::false_type{});
+    }
+    for (; it < ntiles; it += 2) {
+      step(it, S0{}, std::true_type{});
+      if (it + 1 < ntiles) step(it + 1, S1{}, std::true_type{});
     }
   };
   if constexpr (kSplit) {
@@ -514,7 +564,10 @@ void fwd_kernel(const FwdParams p) {
       staged_pair(ntiles - 1, w, o);
 #pragma unroll
       for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
-      while (zj.pending()) zero_store();
+      while (zr.pending()) zero_batch();
+      zr.tail(lane_off, lane_key, [&](uint32_t vo, uint32_t so) {
+        buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rz, vo, so);
+      });
     }
     if (!vec) {  // element-wise zero triangle for unaligned rows
       const int z0 = min(p.N, wtiles * BN);
