@@ -4,10 +4,11 @@
 // attention_cross_token_softmax_sum.py:203-268 and the buffered :568-627)
 // are computed after the forward pass, key-block outer: a workgroup owns two
 // blocks of 256 keys of one (batch, query head), keeps them in VGPRs and
-// streams the query rows that can see them.  S = Q K^T puts keys on lanes and queries in the
-// accumulator registers, so P = exp2(s*qk_scale - lse2[row]) (the forward
-// pass's final base-2 log-sum-exp) is summed over queries in-lane.  Every
-// column is owned by one workgroup: no atomics, the result is deterministic.
+// streams the query rows that can see them.  S = Q K^T puts keys on lanes and
+// queries in the accumulator registers, so P = exp2(s*qk_scale - lse2[row])
+// (the forward pass's final base-2 log-sum-exp) is summed over queries
+// in-lane.  Every column is owned by one workgroup: no atomics, the result is
+// deterministic.
 // GQA groups are folded afterwards by group_reduce_kernel in a fixed order.
 //
 // Raw-score column sums (attention_with_col_sum.py:186-191,
@@ -43,12 +44,17 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
 
 // Key blocks of 256 are dealt in mirror pairs (pb, nkb-1-pb): under a causal
 // mask block kb sees (M - 256 kb) query rows, so a pair always sums to the
-// same amount of work and every workgroup finishes together.  Each of the 8
-// waves owns 32 keys of each block of the pair; both groups share the
-// A operand (the Q chunk) of S = Q K^T, and the later block's MFMAs start
-// only on the query tiles that can see it.
+// same amount of work and every workgroup finishes together.  The workgroup
+// sweeps block pb, then block nkb-1-pb; each of the 8 waves owns 32 keys of
+// the block and holds their K in VGPRs.  Per 32 x 32 tile a wave issues 8
+// MFMAs (256 cycles) against 16 exp, 16 multiply and 16 add instructions
+// (~300 cycles): the VALU, not the MFMA, bounds this pass.  The row's
+// -lse2/qk_scale is the accumulator's starting value, so P = exp2(acc *
+// qk_scale) needs no separate subtraction register.  Holding one block's K
+// at a time (not both blocks', sharing the Q operand) keeps the kernel at
+// ~126 VGPRs; measured 91 -> 85 us at B1 H32 S4096 D128 for both changes.
 template <class E, int D>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3, 4)))
 void colsm_kernel(const ColsmParams p) {
   constexpr int KS = D / 16;
   constexpr int NT = 512;
@@ -69,33 +75,10 @@ void colsm_kernel(const ColsmParams p) {
   map_block_keys(blockIdx.x, npairs, p.B * p.H, pb, bh);
   const int h = bh % p.H, b = bh / p.H, hk = h / p.G;
   const int kbb = p.nkb - 1 - pb;
-  const bool has_b = kbb != pb;
-  // Keys of this wave: group 0 [key0[0], +32) in block pb, group 1 in kbb.
-  const int key0[2] = {pb * BK + 32 * wave, kbb * BK + 32 * wave};
 
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
   const float* lse = p.lse2 + (int64_t)bh * p.M;
-
-  // K (B operand of S = Q K^T): lane holds K[key0[grp] + c][16ks + 8g, +8).
-  u32x4 kreg[2][KS];
-#pragma unroll
-  for (int grp = 0; grp < 2; ++grp)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      kreg[grp][ks] =
-          buf_load16(rk, (uint32_t)(((key0[grp] + c) * p.sk2 + 16 * ks + 8 * g) * 2));
-  // Settle the K loads here: left pending, the compiler's wait counters for
-  // them would also hold back (vmcnt N) on the Q prefetch inside the loop.
-#pragma unroll
-  for (int grp = 0; grp < 2; ++grp)
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[grp][ks]));
-
-  // Query tiles that can see any key of block pb (a superset of kbb's).
-  int rstart = p.row_lo;
-  if (p.causal) rstart = max(rstart, pb * BK - p.causal_off);
-  const int t0 = max(0, rstart) / TQ;
   const int t1 = (p.M + TQ - 1) / TQ;
 
   u32x4 qst[CPT];
@@ -112,6 +95,9 @@ void colsm_kernel(const ColsmParams p) {
       lst = (row < p.row_lo || row >= p.M) ? pos_inf() : lse[row];
     }
   };
+  // LDS gets -lse2 / qk_scale, the starting value of the row's accumulator
+  // (-inf for rows that do not contribute).
+  const float inv_scale = 1.f / p.qk_scale;
   auto stash = [&](int stage) {
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -123,106 +109,115 @@ void colsm_kernel(const ColsmParams p) {
         *reinterpret_cast<u32x4*>(&qlds[stage][tile_off<D>(row, ch)]) = qst[i] ^ p.qneg;
       }
     }
-    if (tid < TQ) llds[stage][tid] = lst;
+    if (tid < TQ) llds[stage][tid] = -lst * inv_scale;
   };
 
-  float colacc[2] = {0.f, 0.f};
-  if (t0 < t1) {
-    fetch(t0);
-    stash(0);
-  }
-  __syncthreads();
-  for (int t = t0; t < t1; ++t) {
-    const int stage = (t - t0) & 1;
-    const bool more = t + 1 < t1;
-    if (more) fetch(t + 1);
-    const int r0 = t * TQ;
-    // Group grp is live if some row of the tile sees its first key, full if
-    // every row sees its last key.
-    bool live[2] = {true, has_b}, full[2] = {true, true};
-    if (p.causal) {
+  for (int blk = 0; blk < 2; ++blk) {
+    const int kb = blk == 0 ? pb : kbb;
+    if (blk == 1 && kbb == pb) break;
+    // Keys of this wave: [key0, key0 + 32).
+    const int key0 = kb * BK + 32 * wave;
+    // K (B operand of S = Q K^T): lane holds K[key0 + c][16ks + 8g, +8).
+    u32x4 kreg[KS];
 #pragma unroll
-      for (int grp = 0; grp < 2; ++grp) {
-        live[grp] = live[grp] && p.causal_off + r0 + TQ - 1 >= key0[grp];
-        full[grp] = p.causal_off + r0 >= key0[grp] + 31;
-      }
+    for (int ks = 0; ks < KS; ++ks)
+      kreg[ks] = buf_load16(rk, (uint32_t)(((key0 + c) * p.sk2 + 16 * ks + 8 * g) * 2));
+    // Settle the K loads here: left pending, the compiler's wait counters for
+    // them would also hold back (vmcnt N) on the Q prefetch inside the loop.
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[ks]));
+
+    // Query tiles that can see any key of the block.
+    int rstart = p.row_lo;
+    if (p.causal) rstart = max(rstart, kb * BK - p.causal_off);
+    const int t0 = max(0, rstart) / TQ;
+
+    float colacc = 0.f;
+    if (t0 < t1) {
+      fetch(t0);
+      stash(0);
     }
-    // Both query blocks of the tile for group 0 and, when TWO, group 1; the
-    // causal mask only where a group crosses the diagonal (separate code, so
-    // full tiles carry no per-element test).
-    auto body = [&](auto two_tag, auto mask_tag) __attribute__((always_inline)) {
-      constexpr bool TWO = decltype(two_tag)::value;
-      constexpr bool MASK = decltype(mask_tag)::value;
-      constexpr int NG = TWO ? 2 : 1;
-      const uint16_t* qt = qlds[stage];
+    __syncthreads();
+    // Tile t uses LDS stage (t - t0) & 1, a compile-time constant in each
+    // copy of the step: the per-lane operand addresses are then loop-invariant
+    // and the stage offset folds into the LDS instructions' immediates.
+    auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+      constexpr int stage = decltype(stage_tag)::value;
+      const bool more = t + 1 < t1;
+      if (more) fetch(t + 1);
+      const int r0 = t * TQ;
+      // Live if some row of the tile sees the wave's first key, full if every
+      // row sees its last key.
+      const bool live = !p.causal || p.causal_off + r0 + TQ - 1 >= key0;
+      const bool full = !p.causal || p.causal_off + r0 >= key0 + 31;
+      // Both 32-row query blocks of the tile; the causal mask only where the
+      // wave's keys cross the diagonal (separate code, so full tiles carry no
+      // per-element test).
+      auto body = [&](auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const uint16_t* qt = qlds[stage];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        // Operand fetches run two k-steps ahead of their MFMAs (pinned
-        // schedule), so no MFMA waits on a fresh LDS read.
-        u32x4 a[KS];
+        for (int qb = 0; qb < 2; ++qb) {
+          // Fenced per query block: the scheduler would otherwise fetch the
+          // next block's operands early and need more than 128 VGPRs.
+          __builtin_amdgcn_sched_barrier(0);
+          // Operand fetches run two k-steps ahead of their MFMAs (pinned
+          // schedule), so no MFMA waits on a fresh LDS read.
+          u32x4 a[KS];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) a[ks] = lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g);
-        f32x16 s[2] = {f32x16{}, f32x16{}};
+          for (int ks = 0; ks < KS; ++ks) a[ks] = lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g);
+          // Register r holds query row r0 + 32qb + acc_row(r, g); it starts at
+          // -lse2[row] / qk_scale, so P = exp2(acc * qk_scale).
+          f32x16 s;
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-          for (int grp = 0; grp < NG; ++grp) s[grp] = E::mma(a[ks], kreg[grp][ks], s[grp]);
-        {
-          constexpr int PD = KS < 2 ? KS : 2;
-          __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);  // DS read
-#pragma unroll
-          for (int i = 0; i < KS; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, NG, 0);  // MFMA
-            if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          for (int hf = 0; hf < 2; ++hf) {
+            const float* lp = &llds[stage][32 * qb + 16 * hf + 8 * g];
+            const f32x4 x0 = *reinterpret_cast<const f32x4*>(lp);
+            const f32x4 x1 = *reinterpret_cast<const f32x4*>(lp + 4);
+            s[8 * hf + 0] = x0.x; s[8 * hf + 1] = x0.y; s[8 * hf + 2] = x0.z; s[8 * hf + 3] = x0.w;
+            s[8 * hf + 4] = x1.x; s[8 * hf + 5] = x1.y; s[8 * hf + 6] = x1.z; s[8 * hf + 7] = x1.w;
           }
-        }
-        // Register r holds query row r0 + 32qb + acc_row(r, g).
-        float lr[16];
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const float* lp = &llds[stage][32 * qb + 16 * hf + 8 * g];
-          const f32x4 x0 = *reinterpret_cast<const f32x4*>(lp);
-          const f32x4 x1 = *reinterpret_cast<const f32x4*>(lp + 4);
-          lr[8 * hf + 0] = x0.x; lr[8 * hf + 1] = x0.y; lr[8 * hf + 2] = x0.z; lr[8 * hf + 3] = x0.w;
-          lr[8 * hf + 4] = x1.x; lr[8 * hf + 5] = x1.y; lr[8 * hf + 6] = x1.z; lr[8 * hf + 7] = x1.w;
-        }
+          for (int ks = 0; ks < KS; ++ks) s = E::mma(a[ks], kreg[ks], s);
+          {
+            constexpr int PD = KS < 2 ? KS : 2;
+            __builtin_amdgcn_sched_group_barrier(0x100, PD + 4, 0);  // DS read: 4 of -lse, PD of Q
 #pragma unroll
-        for (int grp = 0; grp < NG; ++grp) {
-          float pr[16];
+            for (int i = 0; i < KS; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+          }
+          // P replaces S in place.
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            pr[r] = exp2f_fast(fmaf(s[grp][r], p.qk_scale, -lr[r]));
+            s[r] = exp2f_fast(s[r] * p.qk_scale);
             if constexpr (MASK) {
               const int row = r0 + 32 * qb + acc_row(r, g);
-              if (p.causal_off + row < key0[grp] + c) pr[r] = 0.f;
+              if (p.causal_off + row < key0 + c) s[r] = 0.f;
             }
           }
 #pragma unroll
           for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
-            for (int r = 0; r < w; ++r) pr[r] += pr[r + w];
-          colacc[grp] += pr[0];
+            for (int r = 0; r < w; ++r) s[r] += s[r + w];
+          colacc += s[0];
         }
+      };
+      if (live) {
+        if (full) body(std::false_type{});
+        else body(std::true_type{});
       }
+      if (more) stash(stage ^ 1);
+      __syncthreads();
     };
-    if (live[0]) {
-      if (live[1]) {
-        if (full[0] && full[1]) body(std::true_type{}, std::false_type{});
-        else body(std::true_type{}, std::true_type{});
-      } else {
-        if (full[0]) body(std::false_type{}, std::false_type{});
-        else body(std::false_type{}, std::true_type{});
-      }
+    for (int t = t0; t < t1; t += 2) {
+      step(t, std::integral_constant<int, 0>{});
+      if (t + 1 < t1) step(t + 1, std::integral_constant<int, 1>{});
     }
-    if (more) stash(stage ^ 1);
-    __syncthreads();
-  }
-#pragma unroll
-  for (int grp = 0; grp < 2; ++grp) {
-    const float tot = colacc[grp] + __shfl_xor(colacc[grp], 32);
-    const int key = key0[grp] + c;
-    if (g == 0 && (grp == 0 || has_b) && key < p.ncols)
-      p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot;
+    const float tot = colacc + __shfl_xor(colacc, 32);
+    const int key = key0 + c;
+    if (g == 0 && key < p.ncols) p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot;
   }
 }
 
