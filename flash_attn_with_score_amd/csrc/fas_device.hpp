@@ -67,6 +67,19 @@ struct BF16 {
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+// x combined with x of lane l ^ 32: v_permlane32_swap (a VALU lane swap on
+// gfx950) instead of an LDS-routed shuffle.  With both operands x, the pair
+// it returns holds x[l % 32] and x[l % 32 + 32] in every lane.
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, x), false, false);
+  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+__device__ __forceinline__ float xor32_add(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
+                                                  __builtin_bit_cast(unsigned, x), false, false);
+  return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
+}
 __device__ __forceinline__ float log2f_fast(float x) { return __builtin_amdgcn_logf(x); }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));

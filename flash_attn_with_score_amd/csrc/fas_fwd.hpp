@@ -504,7 +504,7 @@ void fwd_kernel(const FwdParams p) {
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        mx = xor32_max(mx);
         const bool grow = mx > m_ref && (m_ref == neg_inf() || (mx - m_ref) * p.qk_scale > 8.f);
         if (__builtin_amdgcn_ballot_w64(grow) != 0) {
           const float m_new = grow ? mx : m_ref;
