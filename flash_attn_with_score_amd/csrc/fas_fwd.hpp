@@ -581,7 +581,7 @@ void fwd_kernel(const FwdParams p) {
   }
 
   // Epilogue: O = acc / l, base-2 LSE, row sums.
-  const float l_tot = l_i + __shfl_xor(l_i, 32);
+  const float l_tot = xor32_add(l_i);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.o + b * p.so0 + h * p.so1, p.o_bytes);
 #pragma unroll
@@ -605,7 +605,7 @@ void fwd_kernel(const FwdParams p) {
           l_tot > 0.f ? m_ref * p.qk_scale + log2f_fast(l_tot) : pos_inf();
   }
   if constexpr (MODE == kFwdRowSum) {
-    const float r = rsum + __shfl_xor(rsum, 32);
+    const float r = xor32_add(rsum);
     if (g == 0 && qrow < p.M) p.aux[b * p.sa0 + h * p.sa1 + (int64_t)qrow * p.sa2] = r * p.sm_scale;
   }
 }

@@ -215,7 +215,7 @@ void colsm_kernel(const ColsmParams p) {
       step(t, std::integral_constant<int, 0>{});
       if (t + 1 < t1) step(t + 1, std::integral_constant<int, 1>{});
     }
-    const float tot = colacc + __shfl_xor(colacc, 32);
+    const float tot = xor32_add(colacc);
     const int key = key0 + c;
     if (g == 0 && key < p.ncols) p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot;
   }
