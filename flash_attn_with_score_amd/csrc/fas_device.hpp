@@ -67,22 +67,45 @@ struct BF16 {
 __device__ __forceinline__ float neg_inf() { return -__builtin_inff(); }
 __device__ __forceinline__ float pos_inf() { return __builtin_inff(); }
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-// x combined with x of lane l ^ 32: v_permlane32_swap (a VALU lane swap on
-// gfx950) instead of an LDS-routed shuffle.  With both operands x, the pair
-// it returns holds x[l % 32] and x[l % 32 + 32] in every lane.
+// The values of lanes l % 32 and l % 32 + 32, in every lane l: one
+// v_permlane32_swap of x with itself (a VALU lane swap on gfx950, not an
+// LDS-routed shuffle).  Both results pass through an empty asm: this
+// compiler's InstCombine folds the intrinsic's second result into its first
+// (it then adds or compares a register with itself).
+__device__ __forceinline__ void lane_halves(float x, float& lo, float& hi) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  unsigned a = r[0], b = r[1];
+  asm volatile("" : "+v"(a), "+v"(b));
+  lo = __builtin_bit_cast(float, a);
+  hi = __builtin_bit_cast(float, b);
+}
+// x combined with x of lane l ^ 32.
+// (A select, not fmaxf: the asm outputs would otherwise be canonicalised
+// first.)
 __device__ __forceinline__ float xor32_max(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
-                                                  __builtin_bit_cast(unsigned, x), false, false);
-  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+  float lo, hi;
+  lane_halves(x, lo, hi);
+  return lo > hi ? lo : hi;
 }
 __device__ __forceinline__ float xor32_add(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, x),
-                                                  __builtin_bit_cast(unsigned, x), false, false);
-  return __builtin_bit_cast(float, r[0]) + __builtin_bit_cast(float, r[1]);
+  float lo, hi;
+  lane_halves(x, lo, hi);
+  return lo + hi;
 }
 __device__ __forceinline__ float log2f_fast(float x) { return __builtin_amdgcn_logf(x); }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Eight 16-bit elements of a 16-byte vector as floats.
+template <class E>
+__device__ __forceinline__ void unpack8(u32x4 v, float (&x)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    x[2 * w] = E::to_f32((uint16_t)(v[w] & 0xffffu));
+    x[2 * w + 1] = E::to_f32((uint16_t)(v[w] >> 16));
+  }
+}
 
 // Buffer descriptor as four SGPR words for inline assembly.
 __device__ __forceinline__ i32x4 make_rsrc_words(const void* base, uint32_t bytes) {
