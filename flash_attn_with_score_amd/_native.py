@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -32,6 +32,7 @@ VARIANT_SOFTMAX_COL_SUM = 4
 VARIANT_CROSS_QK_SUM = 5
 VARIANT_CROSS_SOFTMAX_SUM = 6
 VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7
+VARIANT_ATTENTION_BACKWARD = 8
 
 _I64x4 = ctypes.c_int64 * 4
 _I64x3 = ctypes.c_int64 * 3
@@ -104,6 +105,13 @@ _SIGNATURES = {
         ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_cross_token_softmax_sum_buffered": (
         ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
+    "fas_attention_forward": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_total_attention": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_backward": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x4, ctypes.c_void_p, _I64x3,
+                       ctypes.c_void_p, _I64x4, ctypes.c_void_p, _I64x4, ctypes.c_void_p, _I64x4,
+                       *_WS, ctypes.c_void_p]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -163,8 +163,21 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Workspace {
   size_t lse = 0, part = 0, bsum = 0, region = 0, total = 0;  // byte offsets / total
+  size_t nl = 0, delta = 0;                                     // backward row values
   bool has_lse = false, has_part = false, has_bsum = false, has_region = false;
 };
+
+// Backward: rows padded to whole 128-row blocks.
+int64_t bwd_mpad(const Problem& pr) {
+  return (((int64_t)pr.M + fas::kBwdBlock - 1) / fas::kBwdBlock) * fas::kBwdBlock;
+}
+int64_t bwd_nkb(const Problem& pr) { return ((int64_t)pr.N + fas::kBwdBlock - 1) / fas::kBwdBlock; }
+// The dK/dV kernel walks a KV head's whole query-head group per workgroup
+// unless that leaves fewer workgroups than the chip has CUs; then it takes
+// one query head per workgroup and writes fp32 partials.
+bool bwd_partial(const Problem& pr) {
+  return pr.G > 1 && (int64_t)pr.B * pr.Hk * bwd_nkb(pr) < 256;
+}
 
 // Column count of a variant's side output.
 int64_t ncols_of(int variant, const Problem& pr, int64_t split) {
@@ -200,6 +213,18 @@ Workspace layout(int variant, const Problem& pr, int64_t split) {
     w.region = off;
     const int64_t rows = pr.M > split ? pr.M - split : 0;
     off += align256((size_t)pr.B * pr.H * rows * split * 4);
+  }
+  if (variant == FAS_VARIANT_ATTENTION_BACKWARD) {
+    const size_t rows = (size_t)pr.B * pr.H * bwd_mpad(pr) * 4;
+    w.nl = off;
+    off += align256(rows);
+    w.delta = off;
+    off += align256(rows);
+    if (bwd_partial(pr)) {
+      w.has_part = true;
+      w.part = off;
+      off += align256((size_t)pr.B * pr.H * pr.N * 2 * pr.D * 4);
+    }
   }
   if (raw) {
     const int64_t row_lo = variant == FAS_VARIANT_CROSS_QK_SUM ? split : 0;
@@ -349,7 +374,7 @@ const char* fas_last_error(void) { return g_last_error.c_str(); }
 
 size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
   Problem pr;
-  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED)
+  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_ATTENTION_BACKWARD)
     return (size_t)-1;
   if (check_shape("fas_workspace_bytes", a, &pr)) return (size_t)-1;
   const bool has_split = variant == FAS_VARIANT_CROSS_QK_SUM ||
@@ -437,6 +462,125 @@ int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64
   return run_softmax("fas_attention_cross_token_softmax_sum_buffered",
                      FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED, a, split, cross, st, ws, ws_bytes,
                      stream);
+}
+
+int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3], void* stream) {
+  static const char* fn = "fas_attention_forward";
+  Problem pr;
+  int rc;
+  if ((rc = check_args(fn, a, &pr))) return rc;
+  if ((int64_t)pr.B * pr.H * pr.M == 0) return FAS_OK;
+  if ((rc = check_out3(fn, "lse", lse, st))) return rc;
+  fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
+  p.lse_ln = lse;
+  p.sl0 = st[0];
+  p.sl1 = st[1];
+  p.sl2 = st[2];
+  return run_fwd(fn, p, pr, fas::kFwdPlain, stream);
+}
+
+int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t lst[3],
+                        float* total, const int64_t tst[3], void* stream) {
+  static const char* fn = "fas_total_attention";
+  Problem pr;
+  int rc;
+  if ((rc = check_shape(fn, a, &pr))) return rc;
+  if ((int64_t)pr.B * pr.H * pr.N == 0) return FAS_OK;
+  if ((rc = check_out3(fn, "total", total, tst))) return rc;
+  if (pr.M == 0) return zero_out3(fn, total, tst, pr.B, pr.H, pr.N, stream);
+  if (lse == nullptr || lst == nullptr) return fail(FAS_ERR_INVALID, fn, "lse is NULL");
+  if ((rc = check_tensor(fn, "q", a->q, a->q_stride, pr.M, pr.D))) return rc;
+  if ((rc = check_tensor(fn, "k", a->k, a->k_stride, pr.N, pr.D))) return rc;
+  fas::ColsmParams c{};
+  c.q = static_cast<const uint16_t*>(a->q);
+  c.k = static_cast<const uint16_t*>(a->k);
+  c.lse_ln = lse;
+  c.sl0 = lst[0]; c.sl1 = lst[1]; c.sl2 = lst[2];
+  c.out = total;
+  c.so0 = tst[0]; c.so1 = tst[1]; c.so2 = tst[2];
+  c.sq0 = a->q_stride[0]; c.sq1 = a->q_stride[1]; c.sq2 = a->q_stride[2];
+  c.sk0 = a->k_stride[0]; c.sk1 = a->k_stride[1]; c.sk2 = a->k_stride[2];
+  c.q_bytes = slice_bytes(pr.M, c.sq2, pr.D);
+  c.k_bytes = slice_bytes(pr.N, c.sk2, pr.D);
+  c.qneg = pr.sm_scale < 0.f ? 0x80008000u : 0u;
+  c.B = pr.B; c.H = pr.H; c.G = pr.G; c.M = pr.M; c.N = pr.N;
+  c.row_lo = 0;
+  c.ncols = pr.N;
+  c.causal = pr.causal;
+  c.causal_off = pr.N - pr.M;
+  c.nkb = (pr.N + 255) / 256;
+  c.qk_scale = (float)((double)std::fabs(pr.sm_scale) * 1.4426950408889634);
+  return hip_status(fn, fas::launch_colsm(c, pr.dtype, pr.D, false,
+                                          static_cast<hipStream_t>(stream)));
+}
+
+int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64_t gst[4],
+                           const float* lse, const int64_t lst[3], void* dq,
+                           const int64_t qst[4], void* dk, const int64_t kst[4], void* dv,
+                           const int64_t vst[4], void* ws, size_t ws_bytes, void* stream) {
+  static const char* fn = "fas_attention_backward";
+  Problem pr;
+  int rc;
+  if ((rc = check_args(fn, a, &pr))) return rc;
+  if ((int64_t)pr.B * pr.H == 0) return FAS_OK;
+  if (pr.M > 0) {
+    if (gst == nullptr || qst == nullptr || lst == nullptr || lse == nullptr)
+      return fail(FAS_ERR_INVALID, fn, "dout, dq or lse is NULL");
+    if ((rc = check_tensor(fn, "dout", dout, gst, pr.M, pr.D))) return rc;
+    if ((rc = check_tensor(fn, "dq", dq, qst, pr.M, pr.D))) return rc;
+  }
+  if (pr.N > 0) {
+    if (kst == nullptr || vst == nullptr) return fail(FAS_ERR_INVALID, fn, "dk or dv is NULL");
+    if ((rc = check_tensor(fn, "dk", dk, kst, pr.N, pr.D))) return rc;
+    if ((rc = check_tensor(fn, "dv", dv, vst, pr.N, pr.D))) return rc;
+  }
+  const Workspace w = layout(FAS_VARIANT_ATTENTION_BACKWARD, pr, 0);
+  if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
+  if (pr.M > (1 << 26)) return fail(FAS_ERR_UNSUPPORTED, fn, "seqlen_q exceeds 2^26");
+
+  fas::BwdParams p{};
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.v = static_cast<const uint16_t*>(a->v);
+  p.o = static_cast<const uint16_t*>(a->out);
+  p.dout = static_cast<const uint16_t*>(dout);
+  p.lse = lse;
+  p.nl = at<float>(ws, w.nl);
+  p.delta = at<float>(ws, w.delta);
+  p.dq = static_cast<uint16_t*>(dq);
+  p.dk = static_cast<uint16_t*>(dk);
+  p.dv = static_cast<uint16_t*>(dv);
+  p.part = w.has_part ? at<float>(ws, w.part) : nullptr;
+  p.sq0 = a->q_stride[0]; p.sq1 = a->q_stride[1]; p.sq2 = a->q_stride[2];
+  p.sk0 = a->k_stride[0]; p.sk1 = a->k_stride[1]; p.sk2 = a->k_stride[2];
+  p.sv0 = a->v_stride[0]; p.sv1 = a->v_stride[1]; p.sv2 = a->v_stride[2];
+  p.so0 = a->out_stride[0]; p.so1 = a->out_stride[1]; p.so2 = a->out_stride[2];
+  if (pr.M > 0) {
+    p.sg0 = gst[0]; p.sg1 = gst[1]; p.sg2 = gst[2];
+    p.sdq0 = qst[0]; p.sdq1 = qst[1]; p.sdq2 = qst[2];
+    p.sl0 = lst[0]; p.sl1 = lst[1]; p.sl2 = lst[2];
+  }
+  if (pr.N > 0) {
+    p.sdk0 = kst[0]; p.sdk1 = kst[1]; p.sdk2 = kst[2];
+    p.sdv0 = vst[0]; p.sdv1 = vst[1]; p.sdv2 = vst[2];
+  }
+  p.q_bytes = slice_bytes(pr.M, p.sq2, pr.D);
+  p.k_bytes = slice_bytes(pr.N, p.sk2, pr.D);
+  p.v_bytes = slice_bytes(pr.N, p.sv2, pr.D);
+  p.g_bytes = slice_bytes(pr.M, p.sg2, pr.D);
+  p.qneg = pr.sm_scale < 0.f ? 0x80008000u : 0u;
+  p.B = pr.B; p.H = pr.H; p.G = pr.G; p.Hk = pr.Hk; p.M = pr.M; p.N = pr.N;
+  p.Mpad = (int)bwd_mpad(pr);
+  p.causal = pr.causal;
+  p.causal_off = pr.N - pr.M;
+  p.nkb = (int)bwd_nkb(pr);
+  p.nrb = p.Mpad / fas::kBwdBlock;
+  p.nprep = (p.Mpad + (2048 / pr.D) - 1) / (2048 / pr.D);
+  p.partial = bwd_partial(pr) ? 1 : 0;
+  p.sm_scale = std::fabs(pr.sm_scale);
+  p.scale_signed = pr.sm_scale;
+  p.qk_scale = (float)((double)std::fabs(pr.sm_scale) * 1.4426950408889634);
+  return hip_status(fn, fas::launch_bwd(p, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

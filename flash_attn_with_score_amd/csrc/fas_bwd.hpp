@@ -1,0 +1,485 @@
+// gfx950 backward pass of attention() (flash.py:172-261): dQ, dK and dV from
+// dO, the forward output O and its natural-log normalizer L.
+//
+//   bwd_prep_kernel   per query row: -delta = -sum_d O dO (flash.py:532-578) and
+//                     nl = -L log2(e), the base-2 exponent offset of the row's
+//                     softmax weights (-inf for rows that see no key and for
+//                     the padding rows past M), both into the workspace.
+//   bwd_dkdv_kernel   key-block outer (flash.py:581-755).  A wave owns 32 keys
+//                     and holds their K and V rows in VGPRs as B operands;
+//                     64-row tiles of Q and dO arrive in LDS by DMA.  Per
+//                     32-row block:
+//                       S = Q K^T,  P = exp2(S qk_scale + nl),
+//                       dP - delta = dO V^T (the accumulator starts at -delta),
+//                       dS = P (dP - delta),
+//                       dV^T += dO^T P,  dK^T += Q^T dS.
+//                     Keys sit on lanes, so P and dS leave the accumulator
+//                     directly as B operands; dO^T and Q^T are read from the
+//                     row-major tiles with the transposing LDS load.  GQA: a
+//                     workgroup walks every query head of its KV group, so dK
+//                     and dV are summed over the group in fp32 (the reference
+//                     sums per-head fp16 results, flash.py:258-259).  When
+//                     that leaves too few workgroups for the chip, each
+//                     workgroup takes one query head and writes fp32 partials
+//                     that bwd_dkdv_reduce_kernel adds in head order.
+//   bwd_dq_kernel     query-block outer (flash.py:758-918), the forward pass's
+//                     data flow: a wave owns 32 rows, holds their Q and dO as B
+//                     operands, and streams 64-key tiles of K and V:
+//                       S^T = K Q^T,  P^T,  dP^T - delta = V dO^T,  dS^T,
+//                       dQ^T += K^T dS^T.
+// Masked pairs (causal, keys >= N) get P = 0 and so dS = 0; the products are
+// fp16/bf16 MFMAs with fp32 accumulation, with P and dS rounded to the input
+// type before their products as in the reference (flash.py:687, 721, 904).
+#pragma once
+#include "fas_device.hpp"
+#include "fas_params.hpp"
+
+#include <type_traits>
+
+namespace fas {
+
+constexpr float kLog2e = 1.44269504088896341f;
+
+// LDS DMA of rows [r0, r0 + R) of a row-major (., D) 16-bit matrix into a
+// swizzled R x D LDS tile at byte address lds: 1 KiB blocks dealt to the NW
+// waves; lane l fills physical chunk l % (D/8) of its row, i.e. logical
+// chunk (l % (D/8)) ^ swz(row).  Rows outside the buffer read as zeros.
+template <int D, int R, int NW>
+__device__ __forceinline__ void dma_tile(i32x4 rsrc, int64_t stride, int r0, uint32_t lds,
+                                         int wave, int lane) {
+  constexpr int BLOCKS = R * D / 512;
+  constexpr int RPB = 512 / D;
+  constexpr int CPR = D / 8;
+  constexpr int PER = (BLOCKS + NW - 1) / NW;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int q = wave + i * NW;
+    if (BLOCKS % NW == 0 || q < BLOCKS) {
+      const int row = q * RPB + lane / CPR;
+      const int ch = (lane % CPR) ^ swz<D>(row);
+      dma16(rsrc, (uint32_t)(((r0 + row) * stride + ch * 8) * 2),
+            __builtin_amdgcn_readfirstlane(lds + (uint32_t)(q * 1024)));
+    }
+  }
+}
+
+// Packs accumulator registers 8cs..8cs+7 (contraction indices 8g..8g+7 of
+// k-step cs) as an MFMA B operand.
+template <class E>
+__device__ __forceinline__ u32x4 pack_b(const f32x16& x, int cs) {
+  const int r = 8 * cs;
+  return u32x4{E::pack(x[r + 0], x[r + 1]), E::pack(x[r + 2], x[r + 3]),
+               E::pack(x[r + 4], x[r + 5]), E::pack(x[r + 6], x[r + 7])};
+}
+
+// Eight consecutive fp32 values of LDS row array a starting at index i0 into
+// registers [8hf, 8hf + 8) of x.
+__device__ __forceinline__ void load8(f32x16& x, const float* a, int i0, int hf) {
+  const f32x4 u = *reinterpret_cast<const f32x4*>(a + i0);
+  const f32x4 w = *reinterpret_cast<const f32x4*>(a + i0 + 4);
+  x[8 * hf + 0] = u.x; x[8 * hf + 1] = u.y; x[8 * hf + 2] = u.z; x[8 * hf + 3] = u.w;
+  x[8 * hf + 4] = w.x; x[8 * hf + 5] = w.y; x[8 * hf + 6] = w.z; x[8 * hf + 7] = w.w;
+}
+
+// ---------------------------------------------------------------- prep
+
+template <class E, int D>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdParams p) {
+  constexpr int CPR = D / 8;      // lanes per row
+  constexpr int RPB = 256 / CPR;  // rows per workgroup
+  const int bh = blockIdx.x / p.nprep, b = bh / p.H, h = bh % p.H;
+  const int row = (blockIdx.x % p.nprep) * RPB + (int)threadIdx.x / CPR;
+  const int ch = (int)threadIdx.x % CPR;
+  if (row >= p.Mpad) return;  // whole row groups: the shuffles below stay in range
+  float acc = 0.f;
+  if (row < p.M) {
+    const u32x4 o = *reinterpret_cast<const u32x4*>(p.o + b * p.so0 + h * p.so1 +
+                                                    (int64_t)row * p.so2 + 8 * ch);
+    const u32x4 d = *reinterpret_cast<const u32x4*>(p.dout + b * p.sg0 + h * p.sg1 +
+                                                    (int64_t)row * p.sg2 + 8 * ch);
+    float x[8], y[8];
+    unpack8<E>(o, x);
+    unpack8<E>(d, y);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc = fmaf(x[e], y[e], acc);
+  }
+#pragma unroll
+  for (int w = 1; w < CPR; w <<= 1) acc += __shfl_xor(acc, w);
+  if (ch == 0) {
+    float nl = neg_inf();
+    if (row < p.M) {
+      const float L = p.lse[b * p.sl0 + h * p.sl1 + (int64_t)row * p.sl2];
+      if (L != neg_inf()) nl = -L * kLog2e;
+    }
+    p.nl[(int64_t)bh * p.Mpad + row] = nl;
+    p.delta[(int64_t)bh * p.Mpad + row] = -acc;
+  }
+}
+
+// ---------------------------------------------------------------- dK, dV
+
+template <class E, int D>
+__global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
+  constexpr int KS = D / 16;               // k-steps over the head dim
+  constexpr int DB = D >= 32 ? D / 32 : 1;  // 32-dim blocks of dK^T / dV^T
+  constexpr int NW = 4;
+  constexpr int BK = 32 * NW;              // keys per workgroup
+  constexpr int TQ = 64;                   // query rows per tile
+  constexpr int TILE = TQ * D;
+
+  __shared__ __attribute__((aligned(16))) uint16_t qlds[2][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t glds[2][TILE];  // dO
+  __shared__ __attribute__((aligned(16))) float nlds[2][TQ];
+  __shared__ __attribute__((aligned(16))) float xlds[2][TQ];       // -delta
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, c = lane & 31, g = lane >> 5;
+  // Key blocks ascending (for causal masks, the longest first).
+  const int nrest = p.partial ? p.B * p.H : p.B * p.Hk;
+  const int kb = blockIdx.x / nrest, rest = blockIdx.x % nrest;
+  int b, hk, h0, nheads;
+  if (p.partial) {
+    b = rest / p.H;
+    h0 = rest % p.H;
+    hk = h0 / p.G;
+    nheads = 1;
+  } else {
+    b = rest / p.Hk;
+    hk = rest % p.Hk;
+    h0 = hk * p.G;
+    nheads = p.G;
+  }
+  const int key0 = kb * BK + 32 * wave;  // this wave's keys [key0, key0 + 32)
+
+  // K and V (B operands of S = Q K^T and dP = dO V^T): lane holds row key0 + c,
+  // head dims [16ks + 8g, +8).  Q arrives unchanged by DMA, so K carries the
+  // sign of a negative sm_scale.
+  const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
+  const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + b * p.sv0 + hk * p.sv1, p.v_bytes);
+  u32x4 kreg[KS], vreg[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    kreg[ks] = buf_load16(rk, (uint32_t)(((key0 + c) * p.sk2 + 16 * ks + 8 * g) * 2)) ^ p.qneg;
+    vreg[ks] = buf_load16(rv, (uint32_t)(((key0 + c) * p.sv2 + 16 * ks + 8 * g) * 2));
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[ks]), "+v"(vreg[ks]));
+
+  f32x16 dk[DB], dv[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) {
+    dk[db] = f32x16{};
+    dv[db] = f32x16{};
+  }
+
+  // Query rows that can see a key of the block.
+  const int rstart = p.causal ? max(0, kb * BK - p.causal_off) : 0;
+  const int t0 = rstart / TQ, t1 = (p.M + TQ - 1) / TQ;
+  const float qk = p.qk_scale;
+  const uint32_t q_base = lds_addr(&qlds[0][0]), g_base = lds_addr(&glds[0][0]);
+
+  for (int hh = 0; hh < nheads && t0 < t1; ++hh) {
+    const int h = h0 + hh;
+    const int64_t bh = (int64_t)b * p.H + h;
+    const i32x4 wq = make_rsrc_words(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
+    const i32x4 wg = make_rsrc_words(p.dout + b * p.sg0 + h * p.sg1, p.g_bytes);
+    const float* nlg = p.nl + bh * p.Mpad;
+    const float* xg = p.delta + bh * p.Mpad;
+    float nst = 0.f, xst = 0.f;
+    // Tile t into stage s: Q and dO rows by DMA, the row values by plain loads
+    // (rows < Mpad always: Mpad is a multiple of the tile height).
+    auto fetch = [&](int t, int s) __attribute__((always_inline)) {
+      dma_tile<D, TQ, NW>(wq, p.sq2, t * TQ, q_base + (uint32_t)(s * TILE * 2), wave, lane);
+      dma_tile<D, TQ, NW>(wg, p.sg2, t * TQ, g_base + (uint32_t)(s * TILE * 2), wave, lane);
+      if (tid < TQ) {
+        nst = nlg[t * TQ + tid];
+        xst = xg[t * TQ + tid];
+      }
+    };
+    auto stash = [&](int s) __attribute__((always_inline)) {
+      if (tid < TQ) {
+        nlds[s][tid] = nst;
+        xlds[s][tid] = xst;
+      }
+    };
+    fetch(t0, 0);
+    vm_wait_all();
+    stash(0);
+    __syncthreads();
+    auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+      constexpr int stage = decltype(stage_tag)::value;
+      const bool more = t + 1 < t1;
+      if (more) fetch(t + 1, stage ^ 1);
+      const uint16_t* qt = qlds[stage];
+      const uint16_t* gt = glds[stage];
+      auto body = [&](int qb, auto mask_tag) __attribute__((always_inline)) {
+        constexpr bool MASK = decltype(mask_tag)::value;
+        const int r0 = t * TQ + 32 * qb;
+        // Register r holds query row r0 + acc_row(r, g) and key key0 + c.
+        f32x16 s = f32x16{}, dp;
+        load8(dp, &xlds[stage][32 * qb + 8 * g], 0, 0);
+        load8(dp, &xlds[stage][32 * qb + 16 + 8 * g], 0, 1);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          s = E::mma(lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g), kreg[ks], s);
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+          dp = E::mma(lds_row_chunk<D>(gt, 32 * qb + perm_row(c), ks, g), vreg[ks], dp);
+        f32x16 nl;
+        load8(nl, &nlds[stage][32 * qb + 8 * g], 0, 0);
+        load8(nl, &nlds[stage][32 * qb + 16 + 8 * g], 0, 1);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float pr = exp2f_fast(fmaf(s[r], qk, nl[r]));
+          if constexpr (MASK) {
+            if (p.causal_off + r0 + acc_row(r, g) < key0 + c) pr = 0.f;
+          }
+          s[r] = pr;
+          dp[r] = pr * dp[r];
+        }
+        const u32x4 pb0 = pack_b<E>(s, 0), pb1 = pack_b<E>(s, 1);
+        const u32x4 sb0 = pack_b<E>(dp, 0), sb1 = pack_b<E>(dp, 1);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          dv[db] = E::mma(lds_vt_operand<D>(gt, db, 2 * qb, lane), pb0, dv[db]);
+          dv[db] = E::mma(lds_vt_operand<D>(gt, db, 2 * qb + 1, lane), pb1, dv[db]);
+        }
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          dk[db] = E::mma(lds_vt_operand<D>(qt, db, 2 * qb, lane), sb0, dk[db]);
+          dk[db] = E::mma(lds_vt_operand<D>(qt, db, 2 * qb + 1, lane), sb1, dk[db]);
+        }
+      };
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const int r0 = t * TQ + 32 * qb;
+        // Live if the block's last row sees the wave's first key, full if its
+        // first row sees the wave's last key.
+        const bool live = !p.causal || p.causal_off + r0 + 31 >= key0;
+        const bool full = !p.causal || p.causal_off + r0 >= key0 + 31;
+        if (live) {
+          if (full) body(qb, std::false_type{});
+          else body(qb, std::true_type{});
+        }
+      }
+      if (more) {
+        vm_wait_all();
+        stash(stage ^ 1);
+      }
+      __syncthreads();
+    };
+    for (int t = t0; t < t1; t += 2) {
+      step(t, std::integral_constant<int, 0>{});
+      if (t + 1 < t1) step(t + 1, std::integral_constant<int, 1>{});
+    }
+  }
+
+  // Lane (c, g), register r of block db: key key0 + c, head dim
+  // 32db + acc_row(r, g); registers 8hf..8hf+7 are 8 consecutive dims.
+  const int key = key0 + c;
+  if (key >= p.N) return;
+  const float ks_ = p.scale_signed;
+  if (!p.partial) {
+    uint16_t* dkr = p.dk + b * p.sdk0 + hk * p.sdk1 + (int64_t)key * p.sdk2;
+    uint16_t* dvr = p.dv + b * p.sdv0 + hk * p.sdv1 + (int64_t)key * p.sdv2;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int d0 = 32 * db + 16 * hf + 8 * g;
+        if (d0 < D) {
+          f32x16 x = dk[db] * ks_;
+          *reinterpret_cast<u32x4*>(dkr + d0) = pack_b<E>(x, hf);
+          *reinterpret_cast<u32x4*>(dvr + d0) = pack_b<E>(dv[db], hf);
+        }
+      }
+  } else {
+    float* pr = p.part + (((int64_t)b * p.H + h0) * p.N + key) * (2 * D);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const int d0 = 32 * db + 16 * hf + 8 * g;
+        if (d0 < D) {
+          const f32x16& x = dk[db];
+          const f32x16& y = dv[db];
+          const int r = 8 * hf;
+          *reinterpret_cast<f32x4*>(pr + d0) =
+              f32x4{x[r] * ks_, x[r + 1] * ks_, x[r + 2] * ks_, x[r + 3] * ks_};
+          *reinterpret_cast<f32x4*>(pr + d0 + 4) =
+              f32x4{x[r + 4] * ks_, x[r + 5] * ks_, x[r + 6] * ks_, x[r + 7] * ks_};
+          *reinterpret_cast<f32x4*>(pr + D + d0) = f32x4{y[r], y[r + 1], y[r + 2], y[r + 3]};
+          *reinterpret_cast<f32x4*>(pr + D + d0 + 4) =
+              f32x4{y[r + 4], y[r + 5], y[r + 6], y[r + 7]};
+        }
+      }
+  }
+}
+
+// dK, dV of KV head hk = sum over its G query heads of the fp32 partials, in
+// head order; one thread per 8 elements.
+template <class E, int D>
+__global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(const BwdParams p) {
+  constexpr int CPR = D / 8;
+  const int64_t total = (int64_t)p.B * p.Hk * p.N * CPR;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int ch = (int)(i % CPR);
+    const int64_t r = i / CPR;
+    const int key = (int)(r % p.N);
+    const int64_t bhk = r / p.N;
+    const int hk = (int)(bhk % p.Hk), b = (int)(bhk / p.Hk);
+    float a[8] = {}, v[8] = {};
+    for (int j = 0; j < p.G; ++j) {
+      const float* src = p.part + (((int64_t)b * p.H + hk * p.G + j) * p.N + key) * (2 * D) + 8 * ch;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a[e] += src[e];
+        v[e] += src[D + e];
+      }
+    }
+    const int d0 = 8 * ch;
+    *reinterpret_cast<u32x4*>(p.dk + b * p.sdk0 + hk * p.sdk1 + (int64_t)key * p.sdk2 + d0) =
+        u32x4{E::pack(a[0], a[1]), E::pack(a[2], a[3]), E::pack(a[4], a[5]), E::pack(a[6], a[7])};
+    *reinterpret_cast<u32x4*>(p.dv + b * p.sdv0 + hk * p.sdv1 + (int64_t)key * p.sdv2 + d0) =
+        u32x4{E::pack(v[0], v[1]), E::pack(v[2], v[3]), E::pack(v[4], v[5]), E::pack(v[6], v[7])};
+  }
+}
+
+// ---------------------------------------------------------------- dQ
+
+template <class E, int D>
+__global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
+  constexpr int KS = D / 16;
+  constexpr int DB = D >= 32 ? D / 32 : 1;
+  constexpr int NW = 4;
+  constexpr int BM = 32 * NW;  // query rows per workgroup
+  constexpr int BN = 64;       // keys per tile
+  constexpr int TILE = BN * D;
+
+  __shared__ __attribute__((aligned(16))) uint16_t klds[2][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t vlds[2][TILE];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int nbh = p.B * p.H;
+  int rb = blockIdx.x / nbh;
+  const int bh = blockIdx.x % nbh;
+  if (p.causal) rb = p.nrb - 1 - rb;  // longest row blocks first
+  const int b = bh / p.H, h = bh % p.H, hk = h / p.G;
+  const int row0 = rb * BM, wrow0 = row0 + 32 * wave, qrow = wrow0 + c;
+
+  // Q and dO (B operands of S^T = K Q^T and dP^T = V dO^T): lane holds row
+  // qrow, head dims [16ks + 8g, +8).
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(p.dout + b * p.sg0 + h * p.sg1, p.g_bytes);
+  u32x4 qreg[KS], greg[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    qreg[ks] = buf_load16(rq, (uint32_t)((qrow * p.sq2 + 16 * ks + 8 * g) * 2)) ^ p.qneg;
+    greg[ks] = buf_load16(rg, (uint32_t)((qrow * p.sg2 + 16 * ks + 8 * g) * 2));
+  }
+  // Rows past M read nl = -inf (padding), so their P is 0.
+  const float nl = p.nl[(int64_t)bh * p.Mpad + qrow];
+  const float xl = p.delta[(int64_t)bh * p.Mpad + qrow];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qreg[ks]), "+v"(greg[ks]));
+
+  // Key tiles: [0, ntiles) for the workgroup, [0, wtiles) for this wave,
+  // [0, tfull) without any mask.
+  const int hi = p.causal ? min(p.N, max(0, p.causal_off + row0 + BM)) : p.N;
+  const int ntiles = (hi + BN - 1) / BN;
+  const int whi = p.causal ? min(p.N, max(0, p.causal_off + wrow0 + 32)) : p.N;
+  const int wtiles = (whi + BN - 1) / BN;
+  int tfull = p.N / BN;
+  if (p.causal) tfull = min(tfull, max(0, p.causal_off + wrow0 + 1) / BN);
+
+  const i32x4 wk = make_rsrc_words(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
+  const i32x4 wv = make_rsrc_words(p.v + b * p.sv0 + hk * p.sv1, p.v_bytes);
+  const uint32_t k_base = lds_addr(&klds[0][0]), v_base = lds_addr(&vlds[0][0]);
+  auto fetch = [&](int t, int s) __attribute__((always_inline)) {
+    dma_tile<D, BN, NW>(wk, p.sk2, t * BN, k_base + (uint32_t)(s * TILE * 2), wave, lane);
+    dma_tile<D, BN, NW>(wv, p.sv2, t * BN, v_base + (uint32_t)(s * TILE * 2), wave, lane);
+  };
+
+  f32x16 dq[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dq[db] = f32x16{};
+  const float qk = p.qk_scale;
+
+  if (ntiles > 0) {
+    fetch(0, 0);
+    vm_wait_all();
+    __syncthreads();
+  }
+  auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    constexpr int stage = decltype(stage_tag)::value;
+    const bool more = t + 1 < ntiles;
+    if (more) fetch(t + 1, stage ^ 1);
+    const uint16_t* kt = klds[stage];
+    const uint16_t* vt = vlds[stage];
+    auto body = [&](int kb2, auto mask_tag) __attribute__((always_inline)) {
+      constexpr bool MASK = decltype(mask_tag)::value;
+      const int kbase = t * BN + 32 * kb2;
+      // Register r holds key kbase + acc_row(r, g) for query row qrow.
+      f32x16 s = f32x16{}, dp;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dp[r] = xl;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        s = E::mma(lds_row_chunk<D>(kt, 32 * kb2 + perm_row(c), ks, g), qreg[ks], s);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        dp = E::mma(lds_row_chunk<D>(vt, 32 * kb2 + perm_row(c), ks, g), greg[ks], dp);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float pr = exp2f_fast(fmaf(s[r], qk, nl));
+        if constexpr (MASK) {
+          const int key = kbase + acc_row(r, g);
+          if (key >= p.N || (p.causal && p.causal_off + qrow < key)) pr = 0.f;
+        }
+        dp[r] = pr * dp[r];
+      }
+      const u32x4 sb0 = pack_b<E>(dp, 0), sb1 = pack_b<E>(dp, 1);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        dq[db] = E::mma(lds_vt_operand<D>(kt, db, 2 * kb2, lane), sb0, dq[db]);
+        dq[db] = E::mma(lds_vt_operand<D>(kt, db, 2 * kb2 + 1, lane), sb1, dq[db]);
+      }
+    };
+    if (t < wtiles) {
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+        // Sub-blocks past this wave's last visible key are skipped.
+        if (t * BN + 32 * kb2 < whi) {
+          if (t < tfull) body(kb2, std::false_type{});
+          else body(kb2, std::true_type{});
+        }
+      }
+    }
+    if (more) vm_wait_all();
+    __syncthreads();
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    step(t, std::integral_constant<int, 0>{});
+    if (t + 1 < ntiles) step(t + 1, std::integral_constant<int, 1>{});
+  }
+
+  // Lane (c, g), register r of block db: row qrow, head dim 32db + acc_row(r, g).
+  if (qrow >= p.M) return;
+  uint16_t* dqr = p.dq + b * p.sdq0 + h * p.sdq1 + (int64_t)qrow * p.sdq2;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int d0 = 32 * db + 16 * hf + 8 * g;
+      if (d0 < D) {
+        const f32x16 x = dq[db] * p.scale_signed;
+        *reinterpret_cast<u32x4*>(dqr + d0) = pack_b<E>(x, hf);
+      }
+    }
+}
+
+}  // namespace fas

@@ -600,9 +600,13 @@ void fwd_kernel(const FwdParams p) {
       }
     }
   if (g == 0 && qrow < p.M) {
-    if (p.lse2 != nullptr)
-      p.lse2[(int64_t)bh * p.M + qrow] =
-          l_tot > 0.f ? m_ref * p.qk_scale + log2f_fast(l_tot) : pos_inf();
+    const float lse2 = m_ref * p.qk_scale + log2f_fast(l_tot);
+    if (p.lse2 != nullptr) p.lse2[(int64_t)bh * p.M + qrow] = l_tot > 0.f ? lse2 : pos_inf();
+    // attention()'s log normalizer m * sm_scale + ln(l) (flash.py:477-483).
+    if constexpr (MODE == kFwdPlain)
+      if (p.lse_ln != nullptr)
+        p.lse_ln[b * p.sl0 + h * p.sl1 + (int64_t)qrow * p.sl2] =
+            l_tot > 0.f ? lse2 * 0.69314718055994531f : neg_inf();
   }
   if constexpr (MODE == kFwdRowSum) {
     const float r = xor32_add(rsum);

@@ -20,6 +20,11 @@ hipError_t launch_group_reduce(const float* part, float* out, int64_t so0, int64
 // Raw-score column sums: block sums of q, suffix scan, per-key dot products.
 hipError_t launch_rawsum(const RawParams& p, int dtype, bool suffix, hipStream_t s);
 
+// Backward pass of attention(): prep, dK/dV (+ group reduction), dQ.
+hipError_t launch_bwd(const BwdParams& p, int dtype, int d, hipStream_t s);
+// Rows per dK/dV key block and per dQ row block of the backward kernels.
+constexpr int kBwdBlock = 128;
+
 hipError_t launch_fill_zero(float* p, int64_t s0, int64_t s1, int64_t s2, int64_t n0, int64_t n1,
                             int64_t n2, hipStream_t s);
 

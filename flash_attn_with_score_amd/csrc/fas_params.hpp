@@ -19,6 +19,7 @@ struct FwdParams {
   const uint16_t* v;
   uint16_t* o;
   float* lse2;       // optional (B*H, M) contiguous: m*qk_scale + log2(l), +inf for empty rows
+  float* lse_ln;     // optional (B,H,M) strided: m*sm_scale + ln(l), -inf for empty rows
   uint16_t* scores;  // kFwdScores
   float* aux;        // kFwdRowSum: (B,H,M) strided
   float* region;     // kFwdRegion: (B*H, M - split, split) contiguous fp32
@@ -28,6 +29,7 @@ struct FwdParams {
   int64_t so0, so1, so2;
   int64_t ss0, ss1, ss2;
   int64_t sa0, sa1, sa2;
+  int64_t sl0, sl1, sl2;  // lse_ln strides
   uint32_t q_bytes, k_bytes, v_bytes, o_bytes;  // per-(b, head) buffer extents
   uint32_t qneg;     // 0x80008000 to negate q (negative sm_scale), else 0
   int B, H, G, M, N, split;
@@ -49,6 +51,8 @@ struct ColsmParams {
   const uint16_t* q;
   const uint16_t* k;
   const float* lse2;     // (B*H, M) base-2 LSE from the forward pass
+  const float* lse_ln;   // or, when set, the natural-log normalizer (B,H,M) strided
+  int64_t sl0, sl1, sl2;
   const float* region;   // buffered source: (B*H, M - split, split) raw fp32 scores
   float* out;            // G == 1: (B, Hk, ncols) strided output; else partials (B*H, ncols)
   int64_t sq0, sq1, sq2;
@@ -81,6 +85,42 @@ struct RawParams {
   int causal, causal_off;
   int nextra;            // causal: key blocks below causal_off (all rows admissible)
   float sm_scale;        // signed
+};
+
+// Backward pass of attention() (fas_bwd.hpp).
+struct BwdParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* o;
+  const uint16_t* dout;
+  const float* lse;      // natural-log normalizer L (B,H,M) strided, -inf for empty rows
+  float* nl;             // workspace (B*H, Mpad): -L*log2(e), -inf for rows that see no key
+  float* delta;          // workspace (B*H, Mpad): -sum_d O*dO (0 past M)
+  uint16_t* dq;
+  uint16_t* dk;
+  uint16_t* dv;
+  float* part;           // workspace (B*H, N, 2D) fp32 per-query-head dK | dV (partial mode)
+  int64_t sq0, sq1, sq2;
+  int64_t sk0, sk1, sk2;
+  int64_t sv0, sv1, sv2;
+  int64_t so0, so1, so2;
+  int64_t sg0, sg1, sg2;   // dout
+  int64_t sdq0, sdq1, sdq2;
+  int64_t sdk0, sdk1, sdk2;
+  int64_t sdv0, sdv1, sdv2;
+  int64_t sl0, sl1, sl2;
+  uint32_t q_bytes, k_bytes, v_bytes, g_bytes;
+  uint32_t qneg;          // sign flip of the operand that carries sm_scale's sign
+  int B, H, G, Hk, M, N, Mpad;
+  int causal, causal_off;
+  int nkb;               // 128-key blocks (dK/dV kernel)
+  int nrb;               // 128-row blocks (dQ kernel)
+  int nprep;             // row groups per (b, head) of the prep kernel
+  int partial;           // dK/dV kernel: one query head per workgroup, fp32 partials
+  float sm_scale;        // |sm_scale|
+  float scale_signed;    // sm_scale with its sign: dQ = s sum_j dS_ij k_j, dK = s sum_i dS_ij q_i
+  float qk_scale;        // |sm_scale| * log2(e)
 };
 
 }  // namespace fas

@@ -92,7 +92,16 @@ void colsm_kernel(const ColsmParams p) {
     }
     if (tid < TQ) {
       const int row = t * TQ + tid;
-      lst = (row < p.row_lo || row >= p.M) ? pos_inf() : lse[row];
+      if (row < p.row_lo || row >= p.M) {
+        lst = pos_inf();
+      } else if (p.lse_ln == nullptr) {
+        lst = lse[row];
+      } else {
+        // total_attention(): the caller's natural-log normalizer, -inf for
+        // rows that see no key (total.py:125-128).
+        const float L = p.lse_ln[b * p.sl0 + h * p.sl1 + (int64_t)row * p.sl2];
+        lst = L == neg_inf() ? pos_inf() : L * 1.44269504088896341f;
+      }
     }
   };
   // LDS gets -lse2 / qk_scale, the starting value of the row's accumulator
@@ -270,15 +279,6 @@ __global__ void group_reduce_kernel(const float* __restrict__ part, float* out, 
 }
 
 // ---------------------------------------------------------------- raw sums
-
-template <class E>
-__device__ __forceinline__ void unpack8(u32x4 v, float (&x)[8]) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    x[2 * w] = E::to_f32((uint16_t)(v[w] & 0xffffu));
-    x[2 * w + 1] = E::to_f32((uint16_t)(v[w] >> 16));
-  }
-}
 
 // bsum[bhk][blk][:] = sum over the group's query heads and the rows
 // [row_lo + 64*blk, +64) of q (fp32).

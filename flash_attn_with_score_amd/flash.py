@@ -1,0 +1,98 @@
+"""attention: FlashAttention-2 forward and backward as a torch.autograd.Function.
+
+Drop-in for the reference's flash.py:32-297 (FlashAttention, attention).  The
+forward pass is the family's forward kernel (kFwdPlain) writing O and the
+natural-log normalizer L = m * sm_scale + ln(l) (flash.py:477-483); with
+return_total_attention the key-outer column pass sums the softmax weights per
+query head (total.py:9-48).  The backward pass (flash.py:172-261) runs three
+gfx950 kernels through fas_attention_backward: delta = rowsum(O * dO), the
+key-outer dK/dV kernel and the query-outer dQ kernel.  The reference's
+split-KV forward (flash.py:66-136) is a scheduling choice of its Triton
+kernels for small grids and gives the same O and L.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _common, _native
+
+__all__ = ["attention", "FlashAttention"]
+
+
+def _check_inputs(q, k, v):
+    Dq, Dk, Dv = q.shape[-1], k.shape[-1], v.shape[-1]
+    assert Dq == Dk == Dv, "feature size of q, k, v should be equal"
+    assert Dk in {16, 32, 64, 128}
+    Hk, Hv = k.shape[1], v.shape[1]
+    assert Hk == Hv, "num of heads in k and v should be equal"
+    assert q.shape[1] % Hk == 0, "number of heads in q must be a multiple of that in k & v"
+
+
+def _forward(q, k, v, causal, sm_scale, want_total):
+    p = _common.finish_problem(q, k, v, sm_scale)
+    o = _common.new_output(p.q)
+    L = torch.empty((p.B, p.H, p.M), device=q.device, dtype=torch.float32)
+    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    _common.call("fas_attention_forward", p.q, ctypes.byref(args), L.data_ptr(),
+                 _native.strides3(L))
+    tot = None
+    if want_total:
+        tot = torch.empty((p.B, p.H, p.N), device=q.device, dtype=torch.float32)
+        _common.call("fas_total_attention", p.q, ctypes.byref(args), L.data_ptr(),
+                     _native.strides3(L), tot.data_ptr(), _native.strides3(tot))
+    return p, o, L, tot
+
+
+class FlashAttention(torch.autograd.Function):
+    """flash.py:32-261 without dropout (dropout_p > 0 raises NotImplementedError)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal, sm_scale, dropout_p, return_log_normalizer,
+                return_total_attention, return_seed_offset):
+        _check_inputs(q, k, v)
+        _common.check_device_inputs(q, k, v, dropout_p)
+        p, o, L, tot = _forward(q, k, v, causal, sm_scale, return_total_attention)
+        ctx.save_for_backward(p.q, p.k, p.v, o, L)
+        ctx.sm_scale = p.sm_scale
+        ctx.causal = causal
+        if return_log_normalizer or return_total_attention or return_seed_offset:
+            # Without dropout the reference returns None for seed and offset
+            # (flash.py:161-169).
+            return (o, L if return_log_normalizer else None,
+                    tot if return_total_attention else None, None, None)
+        return o
+
+    @staticmethod
+    def backward(ctx, do, *ignored):
+        q, k, v, o, L = ctx.saved_tensors
+        B, H, M, D = q.shape
+        Hk, N = k.shape[1], k.shape[2]
+        do = _common.as_kernel_operand(do)
+        dq = _common.new_output(q)
+        dk = torch.empty((B, Hk, N, D), dtype=k.dtype, device=q.device)
+        dv = torch.empty((B, Hk, N, D), dtype=v.dtype, device=q.device)
+        args = _native.make_args(q, k, v, o, ctx.causal, ctx.sm_scale)
+        ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args, 0,
+                                                 q.device)
+        _common.call("fas_attention_backward", q, ctypes.byref(args), do.data_ptr(),
+                     _native.strides4(do), L.data_ptr(), _native.strides3(L), dq.data_ptr(),
+                     _native.strides4(dq), dk.data_ptr(), _native.strides4(dk), dv.data_ptr(),
+                     _native.strides4(dv), ws_ptr, ws_bytes)
+        return dq, dk, dv, None, None, None, None, None, None
+
+
+def attention(q, k, v, causal=False, sm_scale=None, dropout_p=0.0,
+              return_log_normalizer=False, return_total_attention=False,
+              return_seed_offset=False):
+    """FlashAttention-2 (flash.py:264-297).
+
+    q (B, Hq, M, D); k, v (B, Hk, N, D) with Hq % Hk == 0; causal masking is
+    bottom-right ((N - M) + i >= j).  Returns out (B, Hq, M, D), or, when any
+    return_* flag is set, (out, log_normalizer (B, Hq, M) fp32 or None,
+    total_attention (B, Hq, N) fp32 or None, seed, offset), seed and offset
+    being None without dropout.  Differentiable in q, k and v.
+    """
+    return FlashAttention.apply(q, k, v, causal, sm_scale, dropout_p, return_log_normalizer,
+                                return_total_attention, return_seed_offset)

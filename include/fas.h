@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define FAS_ABI_VERSION 2
+#define FAS_ABI_VERSION 3
 
 typedef enum fas_dtype {
   FAS_DTYPE_F16 = 0,
@@ -69,7 +69,8 @@ typedef enum fas_variant {
   FAS_VARIANT_SOFTMAX_COL_SUM = 4,
   FAS_VARIANT_CROSS_QK_SUM = 5,
   FAS_VARIANT_CROSS_SOFTMAX_SUM = 6,
-  FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7
+  FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7,
+  FAS_VARIANT_ATTENTION_BACKWARD = 8
 } fas_variant;
 
 /* The attention problem shared by every entry point.  Strides are in
@@ -159,6 +160,37 @@ int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64
                                                    float* cross, const int64_t cross_stride[3],
                                                    void* workspace, size_t workspace_bytes,
                                                    void* stream);
+
+/* Replaces the forward half of flash.py:264-297 (attention ->
+ * FlashAttention.forward :34-170, _fwd_kernel :335-500) without dropout:
+ * out = softmax(mask(q k^T sm_scale)) v, and lse (B, Hq, M) fp32 with
+ * element strides lse_stride receives the natural-log normalizer
+ * m * sm_scale + ln(l), -inf for rows that see no key (flash.py:477-483).
+ * Causal masking is bottom-right, as everywhere but the cross QK sum. */
+int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t lse_stride[3],
+                          void* stream);
+
+/* Replaces total.py:9-48 (+ _total_attention_kernel :51-143), which
+ * flash.py:141-156 runs for return_total_attention: total (B, Hq, N) fp32
+ * receives, per query head and key, the sum over query rows of the softmax
+ * weights exp(q.k * sm_scale - lse) of the admissible pairs.  lse is a
+ * normalizer as fas_attention_forward writes it.  Only a->q and a->k are
+ * read (a->v and a->out may be NULL). */
+int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t lse_stride[3],
+                        float* total, const int64_t total_stride[3], void* stream);
+
+/* Replaces FlashAttention.backward (flash.py:172-261, kernels :532-918)
+ * without dropout.  a->out is the forward output O and lse its normalizer;
+ * dout is dL/dO (shaped like out).  Writes dq (like q) and dk, dv
+ * (B, Hk, N, D) in the input dtype, dk and dv summed over the Hq/Hk query
+ * heads of each KV head.  Needs fas_workspace_bytes(
+ * FAS_VARIANT_ATTENTION_BACKWARD, a, 0) bytes of workspace. */
+int fas_attention_backward(const fas_attn_args* a, const void* dout,
+                           const int64_t dout_stride[4], const float* lse,
+                           const int64_t lse_stride[3], void* dq, const int64_t dq_stride[4],
+                           void* dk, const int64_t dk_stride[4], void* dv,
+                           const int64_t dv_stride[4], void* workspace, size_t workspace_bytes,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -31,6 +31,7 @@ def brute_forward(q, k, v, *, causal: bool, sm_scale: float | None = None,
     out = np.zeros((B, Hq, M, D))
     scores = np.full((B, Hq, M, N), -np.inf)
     weights = np.zeros((B, Hq, M, N))
+    lse = np.full((B, Hq, M), -np.inf)
     for b in range(B):
         for h in range(Hq):
             hk = h // G
@@ -46,6 +47,7 @@ def brute_forward(q, k, v, *, causal: bool, sm_scale: float | None = None,
                 top = max(scores[b, h, i, j] for j in admissible)
                 e = {j: math.exp(scores[b, h, i, j] - top) for j in admissible}
                 total = sum(e.values())
+                lse[b, h, i] = top + math.log(total)
                 for j in admissible:
                     weights[b, h, i, j] = e[j] / total
                 for d in range(D):
@@ -56,6 +58,8 @@ def brute_forward(q, k, v, *, causal: bool, sm_scale: float | None = None,
         "out": out,
         "scores": scores,
         "weights": weights,
+        "lse": lse,
+        "total": weights.sum(axis=2),
         "row_sum": finite.sum(axis=-1),
         "col_sum": np.zeros((B, Hk, N)),
         "col_softmax": np.zeros((B, Hk, N)),

@@ -33,6 +33,13 @@ sums, as the kernels do (attention_with_scores.py:192-195).
 Work is streamed per (batch, head) and per chunk of query rows so the
 largest configurations fit in host memory; per-chunk partial sums are
 accumulated in fp64.
+
+attention_reference restates attention() (flash.py:32-297) in fp64: the
+output, the natural-log normalizer L = m * sm_scale + ln(l) (flash.py:477-483,
+-inf for rows with no admissible key), the per-query-head total attention
+(total.py:120-136) and, given dO, the gradients the backward kernels compute
+(flash.py:172-261), by torch autograd with dK and dV summed over each KV
+head's query-head group (flash.py:258-259).
 """
 from __future__ import annotations
 
@@ -204,3 +211,61 @@ def oracle_for(entry_point: str, q, k, v, *, causal: bool, sm_scale=None, split=
     if side == "scores":
         extra = scores_as_returned(extra)
     return out, extra
+
+
+def attention_reference(q, k, v, do=None, *, causal: bool, sm_scale: float | None = None,
+                        causal_offset: int | None = None) -> dict:
+    """fp64 CPU restatement of attention() and its backward pass.
+
+    Returns out (B,Hq,M,D), lse (B,Hq,M) and total (B,Hq,N) and, when do
+    (shaped like out) is given, dq (like q), dk and dv (like k): the
+    gradients of sum(out * do).  causal_offset defaults to N - M
+    (bottom-right, flash.py:447).
+    """
+    q, k, v = (t.detach().to("cpu", torch.float64) for t in (q, k, v))
+    B, Hq, M, D = q.shape
+    Hk, N = k.shape[1], k.shape[2]
+    assert Hq % Hk == 0
+    G = Hq // Hk
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if causal_offset is None:
+        causal_offset = N - M
+    keep = admissible_mask(0, M, N, causal, causal_offset)
+    has_key = keep.any(dim=1)
+    # Rows with no admissible key use every key in the exponent (finite
+    # values, so autograd stays NaN-free) and are zeroed afterwards.
+    use = keep | ~has_key.unsqueeze(1)
+    res = {
+        "out": torch.zeros(B, Hq, M, D, dtype=torch.float64),
+        "lse": torch.full((B, Hq, M), float("-inf"), dtype=torch.float64),
+        "total": torch.zeros(B, Hq, N, dtype=torch.float64),
+    }
+    grads = do is not None
+    if grads:
+        do = do.detach().to("cpu", torch.float64)
+        res["dq"] = torch.zeros_like(q)
+        res["dk"] = torch.zeros_like(k)
+        res["dv"] = torch.zeros_like(v)
+    row_has = has_key.to(torch.float64).unsqueeze(1)
+    for b in range(B):
+        for hk in range(Hk):
+            hs = slice(hk * G, (hk + 1) * G)
+            qg = q[b, hs].clone().requires_grad_(grads)
+            kk = k[b, hk].clone().requires_grad_(grads)
+            vv = v[b, hk].clone().requires_grad_(grads)
+            s = torch.matmul(qg, kk.transpose(0, 1)) * sm_scale
+            s = s.masked_fill(~use, float("-inf"))
+            lse = torch.logsumexp(s, dim=-1, keepdim=True)
+            p = torch.exp(s - lse) * row_has
+            o = torch.matmul(p, vv)
+            res["out"][b, hs] = o.detach()
+            res["lse"][b, hs] = torch.where(has_key, lse.detach().squeeze(-1),
+                                            torch.full((), float("-inf"), dtype=torch.float64))
+            res["total"][b, hs] = p.detach().sum(dim=1)
+            if grads:
+                gq, gk, gv = torch.autograd.grad(o, (qg, kk, vv), do[b, hs])
+                res["dq"][b, hs] = gq
+                res["dk"][b, hk] = gk
+                res["dv"][b, hk] = gv
+    return res

@@ -1,0 +1,135 @@
+"""GPU parity of attention() (flash.py:32-297) and total_attention (total.py:9-48).
+
+Forward: output within the output tolerance of tests/tolerances.py, the
+natural-log normalizer L within 1e-3 (absolute, or relative to |L| above 1)
+with -inf exactly where a row sees no key, and the per-query-head total
+attention under the sum criterion.  Backward: dq, dk, dv from
+torch.autograd.grad through the autograd Function, within the output
+tolerance of the fp64 oracle gradients (oracle/naive.attention_reference).
+Shapes cover MHA and GQA in both dK/dV modes (whole group per workgroup, and
+per-head fp32 partials when that leaves too few workgroups), every head dim,
+non-divisible lengths, M < N, M > N (rows with no key) and a negative
+sm_scale.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import flash_attn_with_score_amd as fas
+from flash_attn_with_score_amd.total import total_attention
+from oracle import inputs, naive
+from tests.tolerances import assert_out_close, assert_sum_close
+
+pytestmark = pytest.mark.gpu
+
+# (B, Hq, Hk, M, N, D, causal, sm_scale)
+CASES = [
+    (1, 4, 4, 256, 256, 64, True, None),
+    (1, 4, 4, 256, 256, 64, False, None),
+    (2, 4, 2, 200, 300, 128, True, None),     # GQA, per-head partials
+    (1, 8, 1, 130, 100, 32, True, None),      # M > N: rows with no key
+    (1, 2, 2, 77, 333, 16, False, None),
+    (1, 3, 3, 96, 160, 128, True, -0.09),     # negative scale
+    (64, 8, 4, 128, 128, 32, True, None),     # GQA, whole group per workgroup
+    (1, 2, 1, 1, 64, 128, True, None),
+]
+
+
+def _label(c):
+    B, Hq, Hk, M, N, D, causal, sc = c
+    return f"B{B}H{Hq}K{Hk}M{M}N{N}D{D}{'c' if causal else 'f'}{'' if sc is None else 'neg'}"
+
+
+def assert_lse_close(got, ref):
+    got = got.detach().double().cpu()
+    ref = ref.detach().double().cpu()
+    neg = torch.isneginf(ref)
+    assert torch.equal(torch.isneginf(got), neg), "lse: -inf pattern differs"
+    fin = ~neg
+    err = (got[fin] - ref[fin]).abs()
+    bound = 1e-3 * torch.clamp(ref[fin].abs(), min=1.0)
+    assert (err <= bound).all(), f"lse: max err {err.max().item():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("case", CASES, ids=_label)
+def test_attention_forward_and_backward(case, dtype, gpu):
+    B, Hq, Hk, M, N, D, causal, sm_scale = case
+    print(f"[case] attention {_label(case)} {dtype}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=5)
+    g = torch.Generator("cpu").manual_seed(7)
+    do = torch.randn(B, Hq, M, D, generator=g).to(dtype)
+    qd, kd, vd = (t.to(gpu).requires_grad_(True) for t in (q, k, v))
+    o, L, tot, seed, offset = fas.attention(qd, kd, vd, causal=causal, sm_scale=sm_scale,
+                                            return_log_normalizer=True,
+                                            return_total_attention=True)
+    dq, dk, dv = torch.autograd.grad(o, (qd, kd, vd), do.to(gpu))
+    torch.cuda.synchronize()
+    assert seed is None and offset is None
+    ref = naive.attention_reference(q, k, v, do, causal=causal, sm_scale=sm_scale)
+    assert o.dtype == dtype and o.shape == q.shape
+    assert_out_close(o, ref["out"])
+    assert L.dtype == torch.float32 and L.shape == (B, Hq, M)
+    assert_lse_close(L, ref["lse"])
+    assert tot.shape == (B, Hq, N)
+    assert_sum_close(tot, ref["total"], "total")
+    assert dq.dtype == dtype and dq.shape == q.shape
+    assert dk.shape == k.shape and dv.shape == v.shape
+    assert_out_close(dq, ref["dq"], "dq")
+    assert_out_close(dk, ref["dk"], "dk")
+    assert_out_close(dv, ref["dv"], "dv")
+
+
+def test_attention_large_magnitude_inputs(gpu):
+    """q, k, v ~ N(0, 6^2): nearly one-hot softmax rows whose two half-waves
+    see very different maxima."""
+    print("[case] attention large magnitude", flush=True)
+    q, k, v = inputs.make_qkv(1, 4, 2, 256, 256, 128, dtype=torch.float16, seed=12, scale=6.0)
+    g = torch.Generator("cpu").manual_seed(13)
+    do = torch.randn(1, 4, 256, 128, generator=g).to(torch.float16)
+    qd, kd, vd = (t.to(gpu).requires_grad_(True) for t in (q, k, v))
+    o, L, tot, _, _ = fas.attention(qd, kd, vd, causal=True, return_log_normalizer=True,
+                                    return_total_attention=True)
+    dq, dk, dv = torch.autograd.grad(o, (qd, kd, vd), do.to(gpu))
+    torch.cuda.synchronize()
+    ref = naive.attention_reference(q, k, v, do, causal=True)
+    assert_out_close(o, ref["out"])
+    assert_lse_close(L, ref["lse"])
+    assert_sum_close(tot, ref["total"], "total")
+    assert_out_close(dv, ref["dv"], "dv")
+
+
+def test_attention_plain_call_returns_tensor(gpu):
+    q, k, v = inputs.make_qkv(1, 2, 2, 64, 64, 64, dtype=torch.float16, seed=1, device=gpu)
+    o = fas.attention(q, k, v, causal=True)
+    assert isinstance(o, torch.Tensor) and o.shape == q.shape
+
+
+def test_total_attention_module_matches_forward(gpu):
+    """total.total_attention from a saved normalizer equals the forward's
+    return_total_attention output bit for bit (same kernel, same inputs)."""
+    q, k, v = inputs.make_qkv(1, 4, 2, 192, 256, 64, dtype=torch.float16, seed=2, device=gpu)
+    o, L, tot, _, _ = fas.attention(q, k, v, causal=True, return_log_normalizer=True,
+                                    return_total_attention=True)
+    t2 = total_attention(q, k, L, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(tot, t2)
+
+
+def test_attention_backward_metric_shape(gpu):
+    """B1 H32 S1024 D128 fp16 causal: gradients against the fp64 oracle."""
+    B, H, S, D = 1, 32, 1024, 128
+    print("[case] attention backward B1 H32 S1024 D128 f16 causal", flush=True)
+    q, k, v = inputs.make_qkv(B, H, H, S, S, D, dtype=torch.float16, seed=0)
+    g = torch.Generator("cpu").manual_seed(1)
+    do = torch.randn(B, H, S, D, generator=g).to(torch.float16)
+    qd, kd, vd = (t.to(gpu).requires_grad_(True) for t in (q, k, v))
+    o = fas.attention(qd, kd, vd, causal=True)
+    dq, dk, dv = torch.autograd.grad(o, (qd, kd, vd), do.to(gpu))
+    torch.cuda.synchronize()
+    ref = naive.attention_reference(q, k, v, do, causal=True)
+    assert_out_close(o, ref["out"])
+    assert_out_close(dq, ref["dq"], "dq")
+    assert_out_close(dk, ref["dk"], "dk")
+    assert_out_close(dv, ref["dv"], "dv")

@@ -40,7 +40,7 @@ def header_functions():
 
 
 def test_library_loads_with_abi_version(lib):
-    assert lib.fas_abi_version() == _native.ABI_VERSION == 2
+    assert lib.fas_abi_version() == _native.ABI_VERSION == 3
 
 
 def test_exports_match_header(lib):
@@ -51,9 +51,9 @@ def test_exports_match_header(lib):
 
 
 def test_public_api_matches_reference_names():
-    """__init__.py:29-39 of the reference minus flash.attention."""
+    """__init__.py:29-39 of the reference."""
     assert set(fas.__all__) == {
-        "attention_with_scores", "attention_with_row_sum", "attention_with_col_sum",
+        "attention", "attention_with_scores", "attention_with_row_sum", "attention_with_col_sum",
         "attention_with_col_sum_sequential", "attention_with_softmax_col_sum",
         "attention_cross_token_qk_sum", "attention_cross_token_softmax_sum",
         "attention_cross_token_softmax_sum_buffered"}

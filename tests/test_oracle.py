@@ -241,3 +241,82 @@ def test_planted_split_boundary_is_caught():
     with pytest.raises(AssertionError):
         np.testing.assert_allclose(res["cross_softmax"].numpy()[..., :96],
                                    f["cross_softmax"], rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- attention()
+# oracle.naive.attention_reference (flash.py:32-297 and its backward) is
+# pinned by the independent fp64 loop formulation (out, L, total attention)
+# and by central finite differences of sum(out * dO) through that same loop
+# formulation (the gradients).
+
+ATTN_CASES = [  # (B, Hq, Hk, M, N, D, causal)
+    (1, 4, 2, 5, 7, 4, True),
+    (1, 2, 1, 7, 5, 4, True),   # M > N: two rows see no key
+    (2, 2, 2, 4, 6, 3, False),
+]
+
+
+def _attn_inputs(case, seed=3):
+    B, Hq, Hk, M, N, D, causal = case
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=torch.float32, seed=seed)
+    g = torch.Generator("cpu").manual_seed(seed + 100)
+    do = torch.randn(B, Hq, M, D, generator=g, dtype=torch.float32)
+    return q.double(), k.double(), v.double(), do.double(), causal
+
+
+@pytest.mark.parametrize("case", ATTN_CASES)
+def test_attention_reference_forward_matches_brute_force(case):
+    q, k, v, do, causal = _attn_inputs(case)
+    r = naive.attention_reference(q, k, v, causal=causal, sm_scale=0.7)
+    bf = brute.brute_forward(q.numpy(), k.numpy(), v.numpy(), causal=causal, sm_scale=0.7)
+    np.testing.assert_allclose(r["out"].numpy(), bf["out"], atol=1e-12)
+    assert np.array_equal(np.isneginf(r["lse"].numpy()), np.isneginf(bf["lse"]))
+    fin = np.isfinite(bf["lse"])
+    np.testing.assert_allclose(r["lse"].numpy()[fin], bf["lse"][fin], atol=1e-12)
+    np.testing.assert_allclose(r["total"].numpy(), bf["total"], atol=1e-12)
+
+
+def _fd_grads(q, k, v, do, causal, sm_scale, h=1e-6):
+    """Central differences of sum(out * do), out from oracle/brute.py."""
+    qn, kn, vn, dn = (t.numpy().copy() for t in (q, k, v, do))
+
+    def f(qq, kk, vv):
+        return float((brute.brute_forward(qq, kk, vv, causal=causal, sm_scale=sm_scale)["out"]
+                      * dn).sum())
+
+    grads = []
+    for which in range(3):
+        arrs = [qn, kn, vn]
+        base = arrs[which]
+        g = np.zeros_like(base)
+        for idx in np.ndindex(base.shape):
+            old = base[idx]
+            base[idx] = old + h
+            fp = f(*arrs)
+            base[idx] = old - h
+            fm = f(*arrs)
+            base[idx] = old
+            g[idx] = (fp - fm) / (2 * h)
+        grads.append(g)
+    return grads
+
+
+@pytest.mark.parametrize("case", ATTN_CASES)
+def test_attention_reference_gradients_match_finite_differences(case):
+    q, k, v, do, causal = _attn_inputs(case)
+    r = naive.attention_reference(q, k, v, do, causal=causal, sm_scale=0.7)
+    gq, gk, gv = _fd_grads(q, k, v, do, causal, 0.7)
+    np.testing.assert_allclose(r["dq"].numpy(), gq, atol=1e-6)
+    np.testing.assert_allclose(r["dk"].numpy(), gk, atol=1e-6)
+    np.testing.assert_allclose(r["dv"].numpy(), gv, atol=1e-6)
+
+
+def test_planted_gradient_without_group_sum_is_caught():
+    """dK taken from the first query head of each group only (a missing GQA
+    fold in the backward, flash.py:258-259) must fail the finite differences."""
+    case = ATTN_CASES[0]
+    q, k, v, do, causal = _attn_inputs(case)
+    G = q.shape[1] // k.shape[1]
+    r = naive.attention_reference(q[:, ::G], k, v, do[:, ::G], causal=causal, sm_scale=0.7)
+    _, gk, _ = _fd_grads(q, k, v, do, causal, 0.7)
+    assert not np.allclose(r["dk"].numpy(), gk, atol=1e-6)
