@@ -53,6 +53,9 @@ WORKLOADS = {
     "cross_qk": ("attention_cross_token_qk_sum", True, "mfma", 4),
     "cross_softmax": ("attention_cross_token_softmax_sum", True, "mfma", None),
     "cross_softmax_buffered": ("attention_cross_token_softmax_sum_buffered", True, "hbm", None),
+    # attention()'s backward pass alone (flash.py:172-261), FA2 convention:
+    # 2.5x the forward's 4*B*H*D*P.
+    "attention_bwd": ("attention", False, "mfma", 10),
 }
 
 
@@ -87,6 +90,9 @@ def work(name: str, B, H, Hk, M, N, D, causal, split, elem=2):
         return 4 * B * H * D * P, qkvo + 4 * B * H * M
     if name in ("col_sum", "col_sum_sequential", "col_softmax"):
         return fac * B * H * D * P, qkvo + 4 * B * Hk * N
+    if name == "attention_bwd":
+        # reads q, k, v, o, dO, L; writes dq, dk, dv
+        return fac * B * H * D * P, qkvo + elem * (B * H * M * D * 2 + 2 * B * Hk * N * D)
     Px = cross_pairs(M, N, split, causal, off)
     if name == "cross_qk":
         return 4 * B * H * D * P, qkvo + 4 * B * Hk * split
@@ -168,6 +174,14 @@ def measured_traffic(key):
 
 
 def make_call(fas, name, q, k, v, causal, split):
+    if name == "attention_bwd":
+        # One forward outside the timed calls; each call is one backward pass
+        # through the autograd graph (dq, dk, dv).
+        qg, kg, vg = (t.detach().requires_grad_(True) for t in (q, k, v))
+        o = fas.attention(qg, kg, vg, causal=causal)
+        g = torch.Generator(device=q.device).manual_seed(1)
+        do = torch.randn(o.shape, generator=g, device=q.device, dtype=o.dtype)
+        return lambda: torch.autograd.grad(o, (qg, kg, vg), do, retain_graph=True)
     fn = getattr(fas, WORKLOADS[name][0])
     if WORKLOADS[name][1]:
         return lambda: fn(q, k, v, split, causal=causal)
@@ -309,7 +323,7 @@ def main() -> int:
 
     del q, k, v
     torch.cuda.synchronize()
-    if args.cpu_budget > 0:
+    if args.cpu_budget > 0 and args.workload != "attention_bwd":
         line["cpu_baseline"] = cpu_baseline(args.workload, B, H, Hk, M, N, D, causal, split,
                                             dtype, args.cpu_budget)
     else:

@@ -350,7 +350,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(const BwdParams p)
 // ---------------------------------------------------------------- dQ
 
 template <class E, int D>
-__global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_kernel(const BwdParams p) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
   constexpr int NW = 4;
@@ -408,6 +408,8 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
   for (int db = 0; db < DB; ++db) dq[db] = f32x16{};
   const float qk = p.qk_scale;
+  const VtOff vto = vt_offsets<D>(lane);
+  const uint32_t rco = row_chunk_offset<D>(perm_row(c), g);
 
   if (ntiles > 0) {
     fetch(0, 0);
@@ -423,16 +425,36 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
     auto body = [&](int kb2, auto mask_tag) __attribute__((always_inline)) {
       constexpr bool MASK = decltype(mask_tag)::value;
       const int kbase = t * BN + 32 * kb2;
+      // Fenced per sub-block, operand fetches pinned two k-steps ahead of
+      // their MFMAs: left free, the scheduler hoists every fetch of the tile
+      // and the kernel needs more than 256 VGPRs.
+      __builtin_amdgcn_sched_barrier(0);
+      uint32_t ro = rco;
+      opaque(ro);
+      u32x4 ak[KS], av[KS];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        ak[ks] = lds_row_chunk(kt + 32 * kb2 * D, ro, ks);
+        av[ks] = lds_row_chunk(vt + 32 * kb2 * D, ro, ks);
+      }
       // Register r holds key kbase + acc_row(r, g) for query row qrow.
       f32x16 s = f32x16{}, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] = xl;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        s = E::mma(lds_row_chunk<D>(kt, 32 * kb2 + perm_row(c), ks, g), qreg[ks], s);
+      for (int ks = 0; ks < KS; ++ks) {
+        s = E::mma(ak[ks], qreg[ks], s);
+        dp = E::mma(av[ks], greg[ks], dp);
+      }
+      {
+        constexpr int PD = KS < 2 ? KS : 2;
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * PD, 0);  // DS read
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        dp = E::mma(lds_row_chunk<D>(vt, 32 * kb2 + perm_row(c), ks, g), greg[ks], dp);
+        for (int i = 0; i < KS; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+          if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float pr = exp2f_fast(fmaf(s[r], qk, nl));
@@ -443,10 +465,22 @@ __global__ __launch_bounds__(256) void bwd_dq_kernel(const BwdParams p) {
         dp[r] = pr * dp[r];
       }
       const u32x4 sb0 = pack_b<E>(dp, 0), sb1 = pack_b<E>(dp, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      VtOff o = vto;
+      opaque(o);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        dq[db] = E::mma(lds_vt_operand<D>(kt, db, 2 * kb2, lane), sb0, dq[db]);
-        dq[db] = E::mma(lds_vt_operand<D>(kt, db, 2 * kb2 + 1, lane), sb1, dq[db]);
+        dq[db] = E::mma(lds_vt_operand<D>(kt, o, db, 2 * kb2), sb0, dq[db]);
+        dq[db] = E::mma(lds_vt_operand<D>(kt, o, db, 2 * kb2 + 1), sb1, dq[db]);
+      }
+      {
+        // K^T fetches (two transposing reads each) one MFMA ahead.
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * DB; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          if (i + 2 < 2 * DB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
       }
     };
     if (t < wtiles) {

@@ -226,4 +226,50 @@ __device__ __forceinline__ u32x4 lds_vt_operand(const uint16_t* vtile, int db, i
   return u32x4{a.x, a.y, b.x, b.y};
 }
 
+// lds_vt_operand with its per-lane addressing reduced to two registers.  For
+// every head dim the two byte offsets of block db, contraction step cs are
+// those of (0, 0) XOR 64*db, plus 32*D*cs (checked exhaustively over lanes,
+// blocks and steps): one v_xor per fetch instead of 2*DB offset registers
+// held across the loop.  Callers pass the offsets through an empty asm per
+// use region so the XORs are not hoisted back into registers.
+struct VtOff {
+  uint32_t o0, o1;
+};
+template <int D>
+__device__ __forceinline__ VtOff vt_offsets(int lane) {
+  const int g = lane >> 5, half = (lane >> 4) & 1, j = lane & 15;
+  const int jj = j & 3;
+  const int sw = ((jj & 1) << 1) | (jj >> 1);
+  int dim = 16 * half + 4 * sw;
+  if constexpr (D < 32) dim &= D - 1;
+  const int key = 8 * g + (j >> 2);
+  const int ch = dim >> 3, sub = dim & 7;
+  return VtOff{(uint32_t)(2 * (tile_off<D>(key, ch) + sub)),
+               (uint32_t)(2 * (tile_off<D>(key + 4, ch) + sub))};
+}
+template <int D>
+__device__ __forceinline__ u32x4 lds_vt_operand(const uint16_t* vtile, VtOff o, int db, int cs) {
+  const char* t = reinterpret_cast<const char*>(vtile) + 32 * D * cs;
+  const uint32_t m = 64u * (uint32_t)db;
+  const fp16x4_lds r0 =
+      __builtin_amdgcn_ds_read_tr16_b64_v4f16((FAS_LDS fp16x4_lds*)(t + (o.o0 ^ m)));
+  const fp16x4_lds r1 =
+      __builtin_amdgcn_ds_read_tr16_b64_v4f16((FAS_LDS fp16x4_lds*)(t + (o.o1 ^ m)));
+  const u32x2 a = __builtin_bit_cast(u32x2, r0), b = __builtin_bit_cast(u32x2, r1);
+  return u32x4{a.x, a.y, b.x, b.y};
+}
+__device__ __forceinline__ void opaque(VtOff& o) { asm volatile("" : "+v"(o.o0), "+v"(o.o1)); }
+// lds_row_chunk likewise: the byte offset of k-step ks is that of k-step 0
+// XOR 32*ks (also checked exhaustively), and rows 16 apart differ by an
+// immediate because swz depends on row bits 0-3 only.
+template <int D>
+__device__ __forceinline__ uint32_t row_chunk_offset(int row, int g) {
+  return (uint32_t)(2 * tile_off<D>(row, g));
+}
+__device__ __forceinline__ u32x4 lds_row_chunk(const uint16_t* tile, uint32_t off, int ks) {
+  return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(tile) +
+                                         (off ^ (32u * (uint32_t)ks)));
+}
+__device__ __forceinline__ void opaque(uint32_t& o) { asm volatile("" : "+v"(o)); }
+
 }  // namespace fas
