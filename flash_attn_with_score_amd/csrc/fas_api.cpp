@@ -110,6 +110,17 @@ int check_args(const char* fn, const fas_attn_args* a, Problem* pr) {
   return FAS_OK;
 }
 
+// Exponent scale of the base-2 softmax, |sm_scale| * log2(e).  For
+// sm_scale == 0 the weights are uniform over the admissible keys; a zero
+// scale would turn the masked scores' -inf into NaN (-inf * 0) and the
+// column pass's starting value -lse2 / qk_scale into a division by zero, so
+// a tiny positive scale stands in: finite scores then contribute exp2(~0) = 1
+// exactly in fp32, masked ones exp2(-inf) = 0.
+float qk_scale_of(float sm_scale) {
+  if (sm_scale == 0.f) return 1e-30f;
+  return (float)((double)std::fabs(sm_scale) * 1.4426950408889634);
+}
+
 // Fills the forward parameter block.  top_left selects the cross-token
 // QK-sum's causal alignment (i >= j) instead of (N - M) + i >= j.
 fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_left, int rows_per_block) {
@@ -136,7 +147,7 @@ fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_le
   p.causal_off = top_left ? 0 : pr.N - pr.M;
   p.nrb = (pr.M + rows_per_block - 1) / rows_per_block;
   p.sm_scale = std::fabs(pr.sm_scale);
-  p.qk_scale = (float)((double)std::fabs(pr.sm_scale) * 1.4426950408889634);
+  p.qk_scale = qk_scale_of(pr.sm_scale);
   return p;
 }
 
@@ -509,7 +520,7 @@ int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t 
   c.causal = pr.causal;
   c.causal_off = pr.N - pr.M;
   c.nkb = (pr.N + 255) / 256;
-  c.qk_scale = (float)((double)std::fabs(pr.sm_scale) * 1.4426950408889634);
+  c.qk_scale = qk_scale_of(pr.sm_scale);
   return hip_status(fn, fas::launch_colsm(c, pr.dtype, pr.D, false,
                                           static_cast<hipStream_t>(stream)));
 }
@@ -579,7 +590,7 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   p.partial = bwd_partial(pr) ? 1 : 0;
   p.sm_scale = std::fabs(pr.sm_scale);
   p.scale_signed = pr.sm_scale;
-  p.qk_scale = (float)((double)std::fabs(pr.sm_scale) * 1.4426950408889634);
+  p.qk_scale = qk_scale_of(pr.sm_scale);
   return hip_status(fn, fas::launch_bwd(p, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
 }
 

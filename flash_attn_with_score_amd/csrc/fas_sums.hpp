@@ -53,7 +53,10 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
 // qk_scale) needs no separate subtraction register.  Holding one block's K
 // at a time (not both blocks', sharing the Q operand) keeps the kernel at
 // ~126 VGPRs; measured 91 -> 85 us at B1 H32 S4096 D128 for both changes.
-template <class E, int D>
+// LN: the row offsets come from a natural-log normalizer (p.lse_ln,
+// total_attention) instead of the forward's base-2 LSE; a template flag so
+// the default copy carries no conversion code in its loop.
+template <class E, int D, bool LN>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3, 4)))
 void colsm_kernel(const ColsmParams p) {
   constexpr int KS = D / 16;
@@ -94,7 +97,7 @@ void colsm_kernel(const ColsmParams p) {
       const int row = t * TQ + tid;
       if (row < p.row_lo || row >= p.M) {
         lst = pos_inf();
-      } else if (p.lse_ln == nullptr) {
+      } else if constexpr (!LN) {
         lst = lse[row];
       } else {
         // total_attention(): the caller's natural-log normalizer, -inf for

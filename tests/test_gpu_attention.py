@@ -33,12 +33,14 @@ CASES = [
     (1, 3, 3, 96, 160, 128, True, -0.09),     # negative scale
     (64, 8, 4, 128, 128, 32, True, None),     # GQA, whole group per workgroup
     (1, 2, 1, 1, 64, 128, True, None),
+    (1, 4, 2, 64, 96, 64, True, 0.0),         # zero scale: uniform weights
 ]
 
 
 def _label(c):
     B, Hq, Hk, M, N, D, causal, sc = c
-    return f"B{B}H{Hq}K{Hk}M{M}N{N}D{D}{'c' if causal else 'f'}{'' if sc is None else 'neg'}"
+    tag = "" if sc is None else ("zero" if sc == 0 else "neg")
+    return f"B{B}H{Hq}K{Hk}M{M}N{N}D{D}{'c' if causal else 'f'}{tag}"
 
 
 def assert_lse_close(got, ref):

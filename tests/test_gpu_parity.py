@@ -49,20 +49,21 @@ def _label(shape):
     return "B{}H{}K{}M{}N{}D{}".format(*shape)
 
 
-def _run(ep, shape, dtype, causal, gpu, split=None, seed=0, scale=1.0):
+def _run(ep, shape, dtype, causal, gpu, split=None, seed=0, scale=1.0, sm_scale=None):
     B, Hq, Hk, M, N, D = shape
-    print(f"[case] {ep} {_label(shape)} {dtype} causal={causal} split={split} scale={scale}",
-          flush=True)
+    print(f"[case] {ep} {_label(shape)} {dtype} causal={causal} split={split} scale={scale} "
+          f"sm_scale={sm_scale}", flush=True)
     q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=seed, scale=scale)
     fn = getattr(fas, ep)
     qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
     if split is None:
-        out, extra = fn(qd, kd, vd, causal=causal)
+        out, extra = fn(qd, kd, vd, causal=causal, sm_scale=sm_scale)
     else:
-        out, extra = fn(qd, kd, vd, split, causal=causal)
+        out, extra = fn(qd, kd, vd, split, causal=causal, sm_scale=sm_scale)
     torch.cuda.synchronize()
     side = naive.ENTRY_POINT_OUTPUT[ep]
-    ref = naive.reference_forward(q, k, v, causal=causal, causal_offset=naive.ENTRY_POINT_OFFSET[ep],
+    ref = naive.reference_forward(q, k, v, causal=causal, sm_scale=sm_scale,
+                                  causal_offset=naive.ENTRY_POINT_OFFSET[ep],
                                   split=split, want=("out", side))
     assert out.dtype == dtype and out.shape == q.shape
     assert_out_close(out, ref["out"])
@@ -80,6 +81,16 @@ def _run(ep, shape, dtype, causal, gpu, split=None, seed=0, scale=1.0):
 @pytest.mark.parametrize("ep", PLAIN_EPS)
 def test_plain_entry_points(ep, shape, dtype, causal, gpu):
     _run(ep, shape, dtype, causal, gpu)
+
+
+@pytest.mark.parametrize("sm_scale", [0.0, 0.3, -0.2], ids=["zero", "pos", "neg"])
+@pytest.mark.parametrize("ep", PLAIN_EPS + CROSS_EPS)
+def test_explicit_sm_scale(ep, sm_scale, gpu):
+    """sm_scale passed explicitly, including 0 (uniform weights over the
+    admissible keys) and a negative value."""
+    split = 100 if "cross" in ep else None
+    _run(ep, (1, 4, 2, 192, 256, 64), torch.float16, True, gpu, split=split, seed=3,
+         sm_scale=sm_scale)
 
 
 @pytest.mark.parametrize("ep", PLAIN_EPS + ["attention_cross_token_softmax_sum"])
