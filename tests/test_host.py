@@ -94,6 +94,51 @@ def test_workspace_sizes(lib):
         r256(B * 4 * M * 4)
 
 
+def test_attention_backward_workspace(lib):
+    """Two (B*Hq, Mpad) fp32 row arrays, Mpad = M rounded up to 128, plus
+    per-query-head fp32 dK|dV partials only when Hq > Hk and the KV-head
+    grid B*Hk*ceil(N/128) is below 256 workgroups."""
+    def r256(x):
+        return (x + 255) // 256 * 256
+
+    B, Hq, Hk, M, N, D = 2, 8, 2, 300, 500, 64
+    a = make_args(B, Hq, Hk, M, N, D)
+    mpad = 384
+    want = 2 * r256(B * Hq * mpad * 4) + r256(B * Hq * N * 2 * D * 4)
+    assert lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0) == want
+    a = make_args(64, 8, 4, 128, 128, 32)  # 64 * 4 * 1 = 256 workgroups: no partials
+    assert lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0) == \
+        2 * r256(64 * 8 * 128 * 4)
+    a = make_args(1, 4, 4, 100, 100, 128)  # MHA: no partials
+    assert lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0) == \
+        2 * r256(4 * 128 * 4)
+
+
+def test_attention_entry_points_reject_bad_requests(lib):
+    a = make_args()
+    st3 = _native._I64x3(300, 1, 1)
+    st4 = _native._I64x4(4 * 300 * 128, 300 * 128, 128, 1)
+    kst = _native._I64x4(2 * 300 * 128, 300 * 128, 128, 1)
+    # forward: the normalizer output is required
+    assert lib.fas_attention_forward(ctypes.byref(a), None, st3, None) == _native.FAS_ERR_INVALID
+    assert "fas_attention_forward" in _err(lib) and "lse" in _err(lib)
+    # backward: a NULL dout, a misaligned dk, a short workspace
+    need = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0)
+    rc = lib.fas_attention_backward(ctypes.byref(a), None, st4, 0x10000, st3, 0x10000, st4,
+                                    0x10000, kst, 0x10000, kst, 0x10000, need, None)
+    assert rc == _native.FAS_ERR_INVALID and "dout is NULL" in _err(lib)
+    rc = lib.fas_attention_backward(ctypes.byref(a), 0x10000, st4, 0x10000, st3, 0x10000, st4,
+                                    0x10008, kst, 0x10000, kst, 0x10000, need, None)
+    assert rc == _native.FAS_ERR_INVALID and "dk rows must be 16-byte aligned" in _err(lib)
+    rc = lib.fas_attention_backward(ctypes.byref(a), 0x10000, st4, 0x10000, st3, 0x10000, st4,
+                                    0x10000, kst, 0x10000, kst, 0x10000, need - 1, None)
+    assert rc == _native.FAS_ERR_WORKSPACE and "fas_attention_backward" in _err(lib)
+    # total attention: unsupported head dim
+    bad = make_args(D=48)
+    rc = lib.fas_total_attention(ctypes.byref(bad), 0x10000, st3, 0x10000, st3, None)
+    assert rc == _native.FAS_ERR_UNSUPPORTED and "head_dim 48" in _err(lib)
+
+
 def test_workspace_rejects_bad_requests(lib):
     a = make_args()
     assert lib.fas_workspace_bytes(_native.VARIANT_CROSS_QK_SUM, ctypes.byref(a), 0) == SIZE_MAX
