@@ -36,6 +36,14 @@ struct F16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
+  // acc + both halves of a packed pair (one v_dot2 against (1, 1)).  Row sums
+  // of fp16-rounded softmax weights stay within a half-ulp (2^-12) of the
+  // fp32 sum; bf16 (2^-9) would not, so only F16 sums packed weights.
+  static constexpr bool kPackedRowSum = true;
+  static __device__ __forceinline__ float sum2(uint32_t x, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), f16x2{(_Float16)1.f, (_Float16)1.f},
+                                  acc, false);
+  }
   // Round-to-nearest-even conversion of two floats packed lo | hi << 16.
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, f16x2));
@@ -52,6 +60,11 @@ struct BF16 {
   static __device__ __forceinline__ f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static constexpr bool kPackedRowSum = false;
+  static __device__ __forceinline__ float sum2(uint32_t x, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x),
+                                           bf16x2{(__bf16)1.f, (__bf16)1.f}, acc, false);
   }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo, hi}, bf16x2));

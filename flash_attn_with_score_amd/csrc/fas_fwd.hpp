@@ -377,23 +377,34 @@ void fwd_kernel(const FwdParams p) {
       s[1] = E::mma(a1[ks], qreg[ks], s[1]);
     }
   };
-  // P = exp2(s*qk_scale - offset), l += rowsum(P), O^T += V^T P^T.
-  auto softmax_pv = [&](const f32x16 (&s)[2], const uint16_t* vt) __attribute__((always_inline)) {
+  // P = exp2(s*qk_scale - offset), packed as the B operands of
+  // O^T += V^T P^T.  Returns the lane's sum of its 32 weights of the tile.
+  // For fp16 the sum is taken from the packed values two at a time (v_dot2
+  // against (1, 1)): the same rounded weights the product uses, at half the
+  // adds; bf16 weights are too coarse for that and are summed in fp32.
+  auto make_p = [&](const f32x16 (&s)[2], u32x4 (&pb)[4]) __attribute__((always_inline)) {
     const float nb = (m_ref == neg_inf() ? 0.f : m_ref) * p.qk_scale;
-    u32x4 pb[4];
+    float lt = 0.f;
 #pragma unroll
     for (int cs = 0; cs < 4; ++cs) {
       const f32x16& sv = s[cs >> 1];
       const int r0 = 8 * (cs & 1);
       float pv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        pv[e] = exp2f_fast(fmaf(sv[r0 + e], p.qk_scale, -nb));
-        l_i += pv[e];
-      }
+      for (int e = 0; e < 8; ++e) pv[e] = exp2f_fast(fmaf(sv[r0 + e], p.qk_scale, -nb));
       pb[cs] = u32x4{E::pack(pv[0], pv[1]), E::pack(pv[2], pv[3]), E::pack(pv[4], pv[5]),
                      E::pack(pv[6], pv[7])};
+      if constexpr (E::kPackedRowSum) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) lt = E::sum2(pb[cs][w], lt);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lt += pv[e];
+      }
     }
+    return lt;
+  };
+  auto pv_mma = [&](const u32x4 (&pb)[4], const uint16_t* vt) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -498,29 +509,60 @@ void fwd_kernel(const FwdParams p) {
           }
         }
 
-        // Online softmax, base 2, on raw scores.
-        float mx = neg_inf();
+        // Online softmax, base 2, on raw scores.  Offset update: the tile
+        // maximum (combined over the two half-waves of a row) raises a row's
+        // offset m_ref when it exceeds it by more than 2^8 in the base-2
+        // exponent, rescaling that row's O and l.
+        auto update_offset = [&]() __attribute__((always_inline)) {
+          float mx = neg_inf();
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-        mx = xor32_max(mx);
-        const bool grow = mx > m_ref && (m_ref == neg_inf() || (mx - m_ref) * p.qk_scale > 8.f);
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-          const float m_new = grow ? mx : m_ref;
-          const float alpha = m_ref == neg_inf() ? 0.f : exp2f_fast((m_ref - m_new) * p.qk_scale);
-          l_i *= alpha;
+            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+          mx = xor32_max(mx);
+          const bool grow =
+              mx > m_ref && (m_ref == neg_inf() || (mx - m_ref) * p.qk_scale > 8.f);
+          if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float m_new = grow ? mx : m_ref;
+            const float alpha =
+                m_ref == neg_inf() ? 0.f : exp2f_fast((m_ref - m_new) * p.qk_scale);
+            l_i *= alpha;
 #pragma unroll
-          for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
-          m_ref = m_new;
+            for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+            m_ref = m_new;
+          }
+        };
+        u32x4 pb[4];
+        float lt;
+        if constexpr (MODE == kFwdScores) {
+          // The score writer updates the offset first: its weights and
+          // O += P V then share one block and overlap, which measured
+          // faster there (229.7 vs 236.9 us at the metric shape).
+          update_offset();
+          lt = make_p(s, pb);
+        } else {
+          // Elsewhere the weights are formed with the current offset first.
+          // Only if some lane's tile weights sum past 2^14 (so a weight
+          // exceeds 2^9: its row maximum rose by more than the 2^8 the
+          // offset may lag) or a row has no offset yet does the wave update
+          // the offset and form the weights again; every weight stays below
+          // 2^14, inside the fp16 range of the product.  This skips the
+          // maximum on nearly every tile (plain forward 144.9 -> 140.3 us).
+          lt = make_p(s, pb);
+          const bool redo = !(lt <= 16384.f) || m_ref == neg_inf();
+          if (__builtin_amdgcn_ballot_w64(redo) != 0) {
+            update_offset();
+            lt = make_p(s, pb);
+          }
         }
+        l_i += lt;
         if constexpr (ST) {
           // O += P V with zero slots in between.
-          softmax_pv(s, vt);
+          pv_mma(pb, vt);
           zero_batch();
           interleave_mfma_stores<kZero>();
         } else {
-          softmax_pv(s, vt);
+          pv_mma(pb, vt);
         }
       } else if constexpr (ST) {
         u32x4 w[8];
