@@ -219,6 +219,8 @@ def main() -> int:
     ap.add_argument("--heads", type=int, default=32)
     ap.add_argument("--kv-heads", type=int, default=None)
     ap.add_argument("--seqlen", type=int, default=4096)
+    ap.add_argument("--seqlen-q", type=int, default=None,
+                    help="query length M (default: --seqlen); keys N = --seqlen")
     ap.add_argument("--head-dim", type=int, default=128)
     ap.add_argument("--split", type=int, default=None)
     ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
@@ -244,8 +246,8 @@ def main() -> int:
     from oracle import inputs
 
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
-    B, H, M, D = args.batch, args.heads, args.seqlen, args.head_dim
-    N = M
+    B, H, N, D = args.batch, args.heads, args.seqlen, args.head_dim
+    M = args.seqlen_q or N
     Hk = args.kv_heads or H
     causal = not args.non_causal
     split = args.split
@@ -297,9 +299,11 @@ def main() -> int:
         "dtype": args.dtype,
         "data": "synthetic: q/k/v i.i.d. N(0,1) from a seeded CPU generator",
         "config": {"workload": f"{WORKLOADS[args.workload][0]} B{B} H{H}/{Hk} "
-                               f"S{M} D{D} {args.dtype} {'causal' if causal else 'full'}"
+                               + (f"S{M}" if M == N else f"M{M} N{N}")
+                               + f" D{D} {args.dtype} {'causal' if causal else 'full'}"
                                + (f" split{split}" if split else ""),
-                   "batch": B, "heads_q": H, "heads_k": Hk, "seqlen": M, "head_dim": D,
+                   "batch": B, "heads_q": H, "heads_k": Hk, "seqlen": M, "seqlen_k": N,
+                   "head_dim": D,
                    "causal": causal, "split": split, "parallelism": "none (1 GPU)"},
         "flop_convention": "4*B*H*D*(admissible pairs) (causal work); "
                            "reference convention 4*B*H*M*N*D in tflops_ref_convention",

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -33,6 +33,7 @@ VARIANT_CROSS_QK_SUM = 5
 VARIANT_CROSS_SOFTMAX_SUM = 6
 VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7
 VARIANT_ATTENTION_BACKWARD = 8
+VARIANT_ATTENTION_FORWARD = 9
 
 _I64x4 = ctypes.c_int64 * 4
 _I64x3 = ctypes.c_int64 * 3
@@ -92,7 +93,8 @@ _SIGNATURES = {
     "fas_last_error": (ctypes.c_char_p, []),
     "fas_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _P(AttnArgs), ctypes.c_int64]),
     "fas_attention_with_scores": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x4, ctypes.c_void_p]),
-    "fas_attention_with_row_sum": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_with_row_sum": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_with_col_sum": (
         ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_with_col_sum_sequential": (
@@ -105,7 +107,8 @@ _SIGNATURES = {
         ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_cross_token_softmax_sum_buffered": (
         ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
-    "fas_attention_forward": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
+    "fas_attention_forward": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_total_attention": (
         ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
     "fas_attention_backward": (

@@ -35,8 +35,11 @@ def attention_with_row_sum(
     _common.check_device_inputs(q, k, v, dropout_p)
     p = _common.finish_problem(q, k, v, sm_scale)
     o = _common.new_output(p.q)
-    row_sum = torch.zeros((B, H, M), device=q.device, dtype=torch.float32)
+    # Every element is written by the kernels (rows with no admissible key get
+    # 0, attention_with_row_sum.py:185), so no zero-fill is needed.
+    row_sum = torch.empty((B, H, M), device=q.device, dtype=torch.float32)
     args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ROW_SUM, args, 0, q.device)
     _common.call("fas_attention_with_row_sum", p.q, ctypes.byref(args), row_sum.data_ptr(),
-                 _native.strides3(row_sum))
+                 _native.strides3(row_sum), ws_ptr, ws_bytes)
     return o, row_sum

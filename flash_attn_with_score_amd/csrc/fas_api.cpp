@@ -146,6 +146,7 @@ fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_le
   p.causal = pr.causal;
   p.causal_off = top_left ? 0 : pr.N - pr.M;
   p.nrb = (pr.M + rows_per_block - 1) / rows_per_block;
+  p.nsplit = 1;
   p.sm_scale = std::fabs(pr.sm_scale);
   p.qk_scale = qk_scale_of(pr.sm_scale);
   return p;
@@ -175,8 +176,47 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct Workspace {
   size_t lse = 0, part = 0, bsum = 0, region = 0, total = 0;  // byte offsets / total
   size_t nl = 0, delta = 0;                                     // backward row values
+  size_t so = 0, sm = 0, sl = 0, sr = 0;                        // key-split partials
   bool has_lse = false, has_part = false, has_bsum = false, has_region = false;
+  bool has_split = false;
 };
+
+// Key split of the plain / row-sum forward.  When the row blocks of the
+// whole problem give fewer workgroups than the chip has CUs (short query
+// ranges against long key ranges: decode, last-window scoring), each row
+// block's key tiles are dealt to nsplit workgroups of at least 4 tiles,
+// aiming at ~512 workgroups in all.  Depends on sizes only, so the workspace
+// query and the launch agree.
+struct SplitPlan {
+  int nsplit = 1, tps = 0;
+  int64_t mpad = 0;
+};
+SplitPlan split_plan(const Problem& pr, bool top_left) {
+  SplitPlan sp;
+  const int64_t nrb = ((int64_t)pr.M + fas::kFwdRows - 1) / fas::kFwdRows;
+  const int64_t wgs = (int64_t)pr.B * pr.H * nrb;
+  if (wgs == 0 || wgs >= 256) return sp;
+  const int64_t off = top_left ? 0 : (int64_t)pr.N - pr.M;
+  int64_t hi = pr.N;
+  if (pr.causal) hi = std::min<int64_t>(pr.N, std::max<int64_t>(0, off + nrb * fas::kFwdRows));
+  const int64_t nt = (hi + 63) / 64;
+  int64_t ns = std::min<int64_t>((512 + wgs - 1) / wgs, nt / 4);
+  if (ns < 2) return sp;
+  const int64_t tps = (nt + ns - 1) / ns;
+  ns = (nt + tps - 1) / tps;
+  if (ns < 2) return sp;
+  sp.nsplit = (int)ns;
+  sp.tps = (int)tps;
+  sp.mpad = nrb * fas::kFwdRows;
+  return sp;
+}
+
+// Whether a variant's forward pass is the plain or row-sum kernel (the ones
+// that can split), and its causal alignment.
+bool forward_can_split(int variant) {
+  return variant != FAS_VARIANT_SCORES && variant != FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED &&
+         variant != FAS_VARIANT_ATTENTION_BACKWARD;
+}
 
 // Backward: rows padded to whole 128-row blocks.
 int64_t bwd_mpad(const Problem& pr) {
@@ -237,6 +277,21 @@ Workspace layout(int variant, const Problem& pr, int64_t split) {
       off += align256((size_t)pr.B * pr.H * pr.N * 2 * pr.D * 4);
     }
   }
+  if (forward_can_split(variant)) {
+    const SplitPlan sp = split_plan(pr, variant == FAS_VARIANT_CROSS_QK_SUM);
+    if (sp.nsplit > 1) {
+      const size_t rows = (size_t)pr.B * pr.H * sp.nsplit * sp.mpad;
+      w.has_split = true;
+      w.so = off;
+      off += align256(rows * pr.D * 4);
+      w.sm = off;
+      off += align256(rows * 4);
+      w.sl = off;
+      off += align256(rows * 4);
+      w.sr = off;
+      off += align256(rows * 4);
+    }
+  }
   if (raw) {
     const int64_t row_lo = variant == FAS_VARIANT_CROSS_QK_SUM ? split : 0;
     const int64_t rows = pr.M > row_lo ? pr.M - row_lo : 0;
@@ -263,6 +318,20 @@ T* at(void* ws, size_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
+// Points the forward at its key-split partials when the plan splits.
+void apply_split(fas::FwdParams& p, const Problem& pr, const Workspace& w, void* ws,
+                 bool top_left) {
+  if (!w.has_split) return;
+  const SplitPlan sp = split_plan(pr, top_left);
+  p.nsplit = sp.nsplit;
+  p.tps = sp.tps;
+  p.Mpad = (int)sp.mpad;
+  p.part_o = at<float>(ws, w.so);
+  p.part_m = at<float>(ws, w.sm);
+  p.part_l = at<float>(ws, w.sl);
+  p.part_r = at<float>(ws, w.sr);
+}
+
 // ---------------------------------------------------------------- variants
 
 // Raw-score column sums (col_sum, col_sum_sequential, cross_qk).
@@ -285,6 +354,7 @@ int run_raw(const char* fn, int variant, const fas_attn_args* a, int64_t split, 
 
   // Attention output.
   fas::FwdParams p = fwd_params(a, pr, cross, fas::kFwdRows);
+  apply_split(p, pr, w, ws, cross);
   if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, stream))) return rc;
   if (pr.M == 0) return zero_out3(fn, out, st, pr.B, pr.Hk, ncols, stream);
 
@@ -328,6 +398,7 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
 
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   p.lse2 = at<float>(ws, w.lse);
+  if (!buffered) apply_split(p, pr, w, ws, false);
   if (buffered) {
     p.region = at<float>(ws, w.region);
     p.split = (int)split;
@@ -385,7 +456,7 @@ const char* fas_last_error(void) { return g_last_error.c_str(); }
 
 size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
   Problem pr;
-  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_ATTENTION_BACKWARD)
+  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_ATTENTION_FORWARD)
     return (size_t)-1;
   if (check_shape("fas_workspace_bytes", a, &pr)) return (size_t)-1;
   const bool has_split = variant == FAS_VARIANT_CROSS_QK_SUM ||
@@ -420,14 +491,17 @@ int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_
 }
 
 int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum, const int64_t st[3],
-                               void* stream) {
+                               void* ws, size_t ws_bytes, void* stream) {
   static const char* fn = "fas_attention_with_row_sum";
   Problem pr;
   int rc;
   if ((rc = check_args(fn, a, &pr))) return rc;
   if ((int64_t)pr.B * pr.H * pr.M == 0) return FAS_OK;
   if ((rc = check_out3(fn, "row_sum", row_sum, st))) return rc;
+  const Workspace w = layout(FAS_VARIANT_ROW_SUM, pr, 0);
+  if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
+  apply_split(p, pr, w, ws, false);
   p.aux = row_sum;
   p.sa0 = st[0];
   p.sa1 = st[1];
@@ -475,14 +549,18 @@ int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64
                      stream);
 }
 
-int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3], void* stream) {
+int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3], void* ws,
+                          size_t ws_bytes, void* stream) {
   static const char* fn = "fas_attention_forward";
   Problem pr;
   int rc;
   if ((rc = check_args(fn, a, &pr))) return rc;
   if ((int64_t)pr.B * pr.H * pr.M == 0) return FAS_OK;
   if ((rc = check_out3(fn, "lse", lse, st))) return rc;
+  const Workspace w = layout(FAS_VARIANT_ATTENTION_FORWARD, pr, 0);
+  if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
+  apply_split(p, pr, w, ws, false);
   p.lse_ln = lse;
   p.sl0 = st[0];
   p.sl1 = st[1];

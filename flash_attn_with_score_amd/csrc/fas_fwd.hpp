@@ -208,8 +208,18 @@ void fwd_kernel(const FwdParams p) {
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
   const bool loader = !kSplit || wave < 4;
 
-  int rb, bh;
-  map_block(blockIdx.x, p.nrb, p.B * p.H, p.causal != 0, rb, bh);
+  // Split over keys: the plain and row-sum modes may give a row block to
+  // nsplit workgroups, each over its own share of the key tiles.
+  constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdRowSum;
+  int rb, bh, split = 0;
+  {
+    int bid = blockIdx.x;
+    if constexpr (kCanSplit) {
+      split = bid % p.nsplit;
+      bid /= p.nsplit;
+    }
+    map_block(bid, p.nrb, p.B * p.H, p.causal != 0, rb, bh);
+  }
   const int h = bh % p.H, b = bh / p.H, hk = h / p.G;
   const int row0 = rb * BM;
   const int wrow0 = row0 + 32 * wave;
@@ -228,6 +238,15 @@ void fwd_kernel(const FwdParams p) {
   };
   const int hi = p.causal ? min(p.N, max(0, p.causal_off + row0 + BM)) : p.N;
   const int ntiles = (hi + BN - 1) / BN;
+  // This workgroup's key tiles [t_begin, t_end): all of them, or one split's
+  // share (possibly none).
+  int t_begin = 0, t_end = ntiles;
+  if constexpr (kCanSplit) {
+    if (p.nsplit > 1) {
+      t_begin = min(ntiles, split * p.tps);
+      t_end = min(ntiles, t_begin + p.tps);
+    }
+  }
   const int wtiles = wtiles_of(wrow0);
   int tfull = p.N / BN;
   if (p.causal) tfull = min(tfull, max(0, p.causal_off + wrow0 + 1) / BN);
@@ -412,7 +431,7 @@ void fwd_kernel(const FwdParams p) {
         oacc[db] = E::mma(lds_vt_operand<D>(vt, db, cs, lane), pb[cs], oacc[db]);
   };
 
-  if (ntiles > 0) issue_tile(0, 0);
+  if (t_begin < t_end) issue_tile(t_begin, 0);
   if (loader) vm_wait_all();
   lds_barrier();
 
@@ -429,7 +448,7 @@ void fwd_kernel(const FwdParams p) {
       constexpr int stage = decltype(stage_tag)::value;
       constexpr bool MK = decltype(mask_tag)::value;
       const bool masked = MK && it >= tfull;
-      if (it + 1 < ntiles) issue_tile(it + 1, stage ^ 1);
+      if (it + 1 < t_end) issue_tile(it + 1, stage ^ 1);
       const uint16_t* kt = kv[stage][0];
       const uint16_t* vt = kv[stage][1];
       const int k0 = it * BN;
@@ -575,20 +594,21 @@ void fwd_kernel(const FwdParams p) {
       if (loader) vm_wait_all();
       lds_barrier();
     };
-    // Tile it uses LDS stage it & 1. Pairs of full tiles first, then the
-    // rest (diagonal and key-edge tiles, and an odd full tile) masked; every
-    // wave runs ntiles steps in all, one workgroup barrier each.
+    // Tile it uses LDS stage (it - t_begin) & 1. Pairs of full tiles first,
+    // then the rest (diagonal and key-edge tiles, and an odd full tile)
+    // masked; every wave runs t_end - t_begin steps in all, one workgroup
+    // barrier each.
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    const int tpairs = min(tfull, ntiles) & ~1;
-    int it = 0;
-    for (; it < tpairs; it += 2) {
+    const int full_end = max(t_begin, min(tfull, t_end));
+    int it = t_begin;
+    for (; it + 1 < full_end; it += 2) {
       step(it, S0{}, std::false_type{});
       step(it + 1, S1{}, std::false_type{});
     }
-    for (; it < ntiles; it += 2) {
+    for (; it < t_end; it += 2) {
       step(it, S0{}, std::true_type{});
-      if (it + 1 < ntiles) step(it + 1, S1{}, std::true_type{});
+      if (it + 1 < t_end) step(it + 1, S1{}, std::true_type{});
     }
   };
   if constexpr (kSplit) {
@@ -624,6 +644,36 @@ void fwd_kernel(const FwdParams p) {
 
   // Epilogue: O = acc / l, base-2 LSE, row sums.
   const float l_tot = xor32_add(l_i);
+  if constexpr (kCanSplit) {
+    if (p.nsplit > 1) {
+      // One split's share: unnormalised O, offset and weight sum (and the
+      // raw row sum) in fp32 for fwd_combine_kernel.
+      const float r_tot = MODE == kFwdRowSum ? xor32_add(rsum) : 0.f;
+      if (qrow < p.M) {
+        const int64_t prow = ((int64_t)bh * p.nsplit + split) * p.Mpad + qrow;
+        float* po = p.part_o + prow * D;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf) {
+            const int d0 = 32 * db + 16 * hf + 8 * g;
+            if (d0 < D) {
+              const f32x16& o = oacc[db];
+              const int r0 = 8 * hf;
+              *reinterpret_cast<f32x4*>(po + d0) = f32x4{o[r0], o[r0 + 1], o[r0 + 2], o[r0 + 3]};
+              *reinterpret_cast<f32x4*>(po + d0 + 4) =
+                  f32x4{o[r0 + 4], o[r0 + 5], o[r0 + 6], o[r0 + 7]};
+            }
+          }
+        if (g == 0) {
+          p.part_m[prow] = m_ref == neg_inf() ? neg_inf() : m_ref * p.qk_scale;
+          p.part_l[prow] = l_tot;
+          if constexpr (MODE == kFwdRowSum) p.part_r[prow] = r_tot;
+        }
+      }
+      return;
+    }
+  }
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.o + b * p.so0 + h * p.so1, p.o_bytes);
 #pragma unroll
@@ -656,10 +706,70 @@ void fwd_kernel(const FwdParams p) {
   }
 }
 
+// Merges the key splits of fwd_kernel: per row, offset M = max over splits,
+// weights 2^(m_s - M), l = sum w_s l_s, O = sum w_s O_s / l, base-2 LSE
+// M + log2 l (+inf for rows that saw no key), and the summed row sums.
+// D/8 threads per row, 8 head dims each.
+template <class E, int D, int MODE>
+__global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdParams p) {
+  constexpr int CPR = D / 8;
+  constexpr int RPB = 256 / CPR;
+  const int nblk = (p.M + RPB - 1) / RPB;
+  const int bh = blockIdx.x / nblk;
+  const int row = (blockIdx.x % nblk) * RPB + (int)threadIdx.x / CPR;
+  const int ch = (int)threadIdx.x % CPR;
+  if (row >= p.M) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const int64_t base = (int64_t)bh * p.nsplit * p.Mpad + row;
+  float mx = neg_inf();
+  // Unrolled so the independent loads of several splits are in flight at once.
+#pragma unroll 8
+  for (int sp = 0; sp < p.nsplit; ++sp) mx = fmaxf(mx, p.part_m[base + (int64_t)sp * p.Mpad]);
+  float l = 0.f, r = 0.f, acc[8] = {};
+#pragma unroll 4
+  for (int sp = 0; sp < p.nsplit; ++sp) {
+    const int64_t pr = base + (int64_t)sp * p.Mpad;
+    if constexpr (MODE == kFwdRowSum) r += p.part_r[pr];
+    const float ms = p.part_m[pr];
+    if (ms == neg_inf()) continue;
+    const float w = exp2f_fast(ms - mx);
+    l = fmaf(w, p.part_l[pr], l);
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(p.part_o + pr * D + 8 * ch);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(p.part_o + pr * D + 8 * ch + 4);
+    acc[0] = fmaf(w, x0.x, acc[0]); acc[1] = fmaf(w, x0.y, acc[1]);
+    acc[2] = fmaf(w, x0.z, acc[2]); acc[3] = fmaf(w, x0.w, acc[3]);
+    acc[4] = fmaf(w, x1.x, acc[4]); acc[5] = fmaf(w, x1.y, acc[5]);
+    acc[6] = fmaf(w, x1.z, acc[6]); acc[7] = fmaf(w, x1.w, acc[7]);
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  *reinterpret_cast<u32x4*>(p.o + b * p.so0 + h * p.so1 + (int64_t)row * p.so2 + 8 * ch) =
+      u32x4{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv),
+            E::pack(acc[4] * inv, acc[5] * inv), E::pack(acc[6] * inv, acc[7] * inv)};
+  if (ch == 0) {
+    const float lse2 = mx + log2f_fast(l);
+    if (p.lse2 != nullptr) p.lse2[(int64_t)bh * p.M + row] = l > 0.f ? lse2 : pos_inf();
+    if constexpr (MODE == kFwdPlain)
+      if (p.lse_ln != nullptr)
+        p.lse_ln[b * p.sl0 + h * p.sl1 + (int64_t)row * p.sl2] =
+            l > 0.f ? lse2 * 0.69314718055994531f : neg_inf();
+    if constexpr (MODE == kFwdRowSum)
+      p.aux[b * p.sa0 + h * p.sa1 + (int64_t)row * p.sa2] = r * p.sm_scale;
+  }
+}
+
 template <class E, int D, int MODE, int NW>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
-  const dim3 grid((unsigned)((int64_t)p.nrb * p.B * p.H)), block(NW * 64);
+  constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdRowSum;
+  const int64_t nsplit = kCanSplit ? p.nsplit : 1;
+  const dim3 grid((unsigned)((int64_t)p.nrb * p.B * p.H * nsplit)), block(NW * 64);
   hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW>), grid, block, 0, stream, p);
+  if constexpr (kCanSplit) {
+    if (p.nsplit > 1 && p.M > 0) {
+      const int64_t nblk = (p.M + 2048 / D - 1) / (2048 / D);
+      hipLaunchKernelGGL((fwd_combine_kernel<E, D, MODE>),
+                         dim3((unsigned)(nblk * p.B * p.H)), dim3(256), 0, stream, p);
+    }
+  }
   return hipGetLastError();
 }
 

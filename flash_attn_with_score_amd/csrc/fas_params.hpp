@@ -38,6 +38,16 @@ struct FwdParams {
   int nrb;           // query row blocks
   int vec_scores;    // scores rows 16-byte aligned and N % 8 == 0
   int vec_region;    // split % 4 == 0
+  // Split over keys (kFwdPlain, kFwdRowSum): nsplit workgroups per row block,
+  // each taking tps key tiles and writing fp32 partials at row pitch Mpad
+  // (= nrb * rows per workgroup); a combine pass merges them.
+  int nsplit;        // 1 = no split
+  int tps;
+  int Mpad;
+  float* part_o;     // (B*H, nsplit, Mpad, D) unnormalised O
+  float* part_m;     // (B*H, nsplit, Mpad) base-2 exponent offset, -inf if none
+  float* part_l;     // (B*H, nsplit, Mpad) sum of the weights
+  float* part_r;     // (B*H, nsplit, Mpad) raw row sums (kFwdRowSum)
   float sm_scale;    // |sm_scale|
   float qk_scale;    // |sm_scale| * log2(e)
 };

@@ -35,8 +35,10 @@ def _forward(q, k, v, causal, sm_scale, want_total):
     o = _common.new_output(p.q)
     L = torch.empty((p.B, p.H, p.M), device=q.device, dtype=torch.float32)
     args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_FORWARD, args, 0,
+                                             q.device)
     _common.call("fas_attention_forward", p.q, ctypes.byref(args), L.data_ptr(),
-                 _native.strides3(L))
+                 _native.strides3(L), ws_ptr, ws_bytes)
     tot = None
     if want_total:
         tot = torch.empty((p.B, p.H, p.N), device=q.device, dtype=torch.float32)

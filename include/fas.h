@@ -31,6 +31,10 @@
  *     zero-fill (the reference zero-fills with torch.zeros).
  *   - Column sums are deterministic: each column is reduced by one
  *     workgroup in a fixed order (the reference uses fp32 atomics).
+ *   - Short query ranges against long key ranges (fewer row blocks than the
+ *     chip has CUs) split each row block's keys over several workgroups;
+ *     the variants whose forward can split then need a workspace for the
+ *     fp32 partials, which fas_workspace_bytes includes.
  *
  * Return value: FAS_OK (0) or a negative fas_status; fas_last_error() then
  * returns a thread-local message naming the entry point and the cause.
@@ -45,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FAS_ABI_VERSION 3
+#define FAS_ABI_VERSION 4
 
 typedef enum fas_dtype {
   FAS_DTYPE_F16 = 0,
@@ -70,7 +74,8 @@ typedef enum fas_variant {
   FAS_VARIANT_CROSS_QK_SUM = 5,
   FAS_VARIANT_CROSS_SOFTMAX_SUM = 6,
   FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7,
-  FAS_VARIANT_ATTENTION_BACKWARD = 8
+  FAS_VARIANT_ATTENTION_BACKWARD = 8,
+  FAS_VARIANT_ATTENTION_FORWARD = 9
 } fas_variant;
 
 /* The attention problem shared by every entry point.  Strides are in
@@ -109,9 +114,12 @@ int fas_attention_with_scores(const fas_attn_args* a, void* scores,
                               const int64_t scores_stride[4], void* stream);
 
 /* Replaces attention_with_row_sum.py:204-326 (+ kernel :22-202).
- * row_sum is (B, Hq, M) fp32: sum over admissible keys of (q.k)*sm_scale. */
+ * row_sum is (B, Hq, M) fp32: sum over admissible keys of (q.k)*sm_scale.
+ * The workspace (fas_workspace_bytes(FAS_VARIANT_ROW_SUM, ...), often 0)
+ * holds key-split partials for short query ranges. */
 int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum,
-                               const int64_t row_sum_stride[3], void* stream);
+                               const int64_t row_sum_stride[3], void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* Replaces attention_with_col_sum.py:297-419 (+ kernel :22-294): col_sum is
  * (B, Hk, N) fp32, sum over admissible queries and group heads of
@@ -166,9 +174,10 @@ int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64
  * out = softmax(mask(q k^T sm_scale)) v, and lse (B, Hq, M) fp32 with
  * element strides lse_stride receives the natural-log normalizer
  * m * sm_scale + ln(l), -inf for rows that see no key (flash.py:477-483).
- * Causal masking is bottom-right, as everywhere but the cross QK sum. */
+ * Causal masking is bottom-right, as everywhere but the cross QK sum.  The
+ * workspace is fas_workspace_bytes(FAS_VARIANT_ATTENTION_FORWARD, ...). */
 int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t lse_stride[3],
-                          void* stream);
+                          void* workspace, size_t workspace_bytes, void* stream);
 
 /* Replaces total.py:9-48 (+ _total_attention_kernel :51-143), which
  * flash.py:141-156 runs for return_total_attention: total (B, Hq, N) fp32

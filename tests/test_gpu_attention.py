@@ -34,6 +34,8 @@ CASES = [
     (64, 8, 4, 128, 128, 32, True, None),     # GQA, whole group per workgroup
     (1, 2, 1, 1, 64, 128, True, None),
     (1, 4, 2, 64, 96, 64, True, 0.0),         # zero scale: uniform weights
+    (1, 4, 2, 32, 2048, 128, True, None),     # key-split forward
+    (1, 2, 2, 600, 512, 32, True, None),      # key-split forward, rows with no key
 ]
 
 

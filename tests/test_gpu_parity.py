@@ -83,6 +83,28 @@ def test_plain_entry_points(ep, shape, dtype, causal, gpu):
     _run(ep, shape, dtype, causal, gpu)
 
 
+# Short query ranges against long key ranges: fewer row blocks than CUs, so
+# the plain and row-sum forward split each row block's keys over several
+# workgroups and merge fp32 partials (including rows with no key, M > N).
+SPLIT_SHAPES = [
+    (1, 4, 2, 32, 2048, 128),
+    (1, 2, 1, 300, 1500, 64),
+    (2, 3, 3, 17, 4000, 16),
+    (1, 2, 2, 600, 512, 32),
+]
+
+
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=_label)
+@pytest.mark.parametrize("ep", [e for e in PLAIN_EPS if e != "attention_with_scores"] + [
+    "attention_cross_token_qk_sum", "attention_cross_token_softmax_sum"])
+def test_key_split_forward(ep, shape, causal, gpu):
+    split = None
+    if "cross" in ep:
+        split = max(1, min(shape[4], shape[3]) // 2)
+    _run(ep, shape, torch.float16, causal, gpu, split=split, seed=9)
+
+
 @pytest.mark.parametrize("sm_scale", [0.0, 0.3, -0.2], ids=["zero", "pos", "neg"])
 @pytest.mark.parametrize("ep", PLAIN_EPS + CROSS_EPS)
 def test_explicit_sm_scale(ep, sm_scale, gpu):

@@ -40,7 +40,7 @@ def header_functions():
 
 
 def test_library_loads_with_abi_version(lib):
-    assert lib.fas_abi_version() == _native.ABI_VERSION == 3
+    assert lib.fas_abi_version() == _native.ABI_VERSION == 4
 
 
 def test_exports_match_header(lib):
@@ -120,7 +120,7 @@ def test_attention_entry_points_reject_bad_requests(lib):
     st4 = _native._I64x4(4 * 300 * 128, 300 * 128, 128, 1)
     kst = _native._I64x4(2 * 300 * 128, 300 * 128, 128, 1)
     # forward: the normalizer output is required
-    assert lib.fas_attention_forward(ctypes.byref(a), None, st3, None) == _native.FAS_ERR_INVALID
+    assert lib.fas_attention_forward(ctypes.byref(a), None, st3, None, 0, None) == _native.FAS_ERR_INVALID
     assert "fas_attention_forward" in _err(lib) and "lse" in _err(lib)
     # backward: a NULL dout, a misaligned dk, a short workspace
     need = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0)
@@ -163,10 +163,10 @@ def test_rejects_unsupported_head_dim(lib):
 def test_rejects_bad_heads_and_dtype(lib):
     a = make_args(Hq=6, Hk=4)
     st = _native._I64x3(1, 1, 1)
-    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None, 0, None) == _native.FAS_ERR_INVALID
     assert "multiple" in _err(lib)
     a = make_args(dtype=7)
-    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == \
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None, 0, None) == \
         _native.FAS_ERR_UNSUPPORTED
 
 
@@ -174,15 +174,15 @@ def test_rejects_null_and_misaligned_tensors(lib):
     st = _native._I64x3(1, 1, 1)
     a = make_args()
     a.q = None
-    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None, 0, None) == _native.FAS_ERR_INVALID
     assert "q is NULL" in _err(lib)
     a = make_args()
     a.k_stride = _native._I64x4(2 * 300 * 128, 300 * 128, 130, 1)  # row stride not a multiple of 8
-    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None, 0, None) == _native.FAS_ERR_INVALID
     assert "k rows must be 16-byte aligned" in _err(lib)
     a = make_args()
     a.v_stride = _native._I64x4(2 * 300 * 128, 300 * 128, 128, 2)
-    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None) == _native.FAS_ERR_INVALID
+    assert lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st, None, 0, None) == _native.FAS_ERR_INVALID
     assert "innermost stride" in _err(lib)
 
 
