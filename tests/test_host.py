@@ -139,6 +139,27 @@ def test_attention_entry_points_reject_bad_requests(lib):
     assert rc == _native.FAS_ERR_UNSUPPORTED and "head_dim 48" in _err(lib)
 
 
+def test_key_split_workspace(lib):
+    """Short query range against long keys: B*Hq*ceil(M/256) = 4 workgroups,
+    32 key tiles -> 8 splits of 4 tiles; partials (B*Hq*8*256) x (D + 3) fp32."""
+    def r256(x):
+        return (x + 255) // 256 * 256
+
+    B, Hq, Hk, M, N, D = 1, 4, 2, 32, 2048, 128
+    a = make_args(B, Hq, Hk, M, N, D)
+    rows = B * Hq * 8 * 256
+    split = r256(rows * D * 4) + 3 * r256(rows * 4)
+    ws = lambda v, s=0: lib.fas_workspace_bytes(v, ctypes.byref(a), s)  # noqa: E731
+    assert ws(_native.VARIANT_ROW_SUM) == split
+    assert ws(_native.VARIANT_ATTENTION_FORWARD) == split
+    assert ws(_native.VARIANT_SOFTMAX_COL_SUM) == (
+        r256(B * Hq * M * 4) + r256(B * Hq * N * 4) + split)
+    assert ws(_native.VARIANT_SCORES) == 0  # the score writer never splits
+    # enough row blocks: no split
+    a = make_args(1, 32, 32, 4096, 4096, 128)
+    assert lib.fas_workspace_bytes(_native.VARIANT_ROW_SUM, ctypes.byref(a), 0) == 0
+
+
 def test_workspace_rejects_bad_requests(lib):
     a = make_args()
     assert lib.fas_workspace_bytes(_native.VARIANT_CROSS_QK_SUM, ctypes.byref(a), 0) == SIZE_MAX
