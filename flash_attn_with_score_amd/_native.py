@@ -92,7 +92,9 @@ _SIGNATURES = {
     "fas_abi_version": (ctypes.c_int, []),
     "fas_last_error": (ctypes.c_char_p, []),
     "fas_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, _P(AttnArgs), ctypes.c_int64]),
-    "fas_attention_with_scores": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x4, ctypes.c_void_p]),
+    "fas_attention_with_scores": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x4, *_WS, ctypes.c_void_p]),
+    "fas_attention_scores": (ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x4, ctypes.c_void_p]),
     "fas_attention_with_row_sum": (
         ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_with_col_sum": (

@@ -43,6 +43,7 @@ def attention_with_scores(
     o = _common.new_output(p.q)
     scores = torch.empty((B, H, M, N), device=q.device, dtype=q.dtype)
     args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_SCORES, args, 0, q.device)
     _common.call("fas_attention_with_scores", p.q, ctypes.byref(args), scores.data_ptr(),
-                 _native.strides4(scores))
+                 _native.strides4(scores), ws_ptr, ws_bytes)
     return o, scores

@@ -213,8 +213,10 @@ SplitPlan split_plan(const Problem& pr, bool top_left) {
 
 // Whether a variant's forward pass is the plain or row-sum kernel (the ones
 // that can split), and its causal alignment.
+// The scores variant takes this route too: for a split plan it runs the
+// plain forward plus the scores-only kernel instead of the fused writer.
 bool forward_can_split(int variant) {
-  return variant != FAS_VARIANT_SCORES && variant != FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED &&
+  return variant != FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED &&
          variant != FAS_VARIANT_ATTENTION_BACKWARD;
 }
 
@@ -466,20 +468,59 @@ size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
   return layout(variant, pr, has_split ? split : 0).total;
 }
 
-int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_t st[4],
-                              void* stream) {
+static int check_scores_out(const char* fn, const void* scores, const int64_t* st) {
+  if (scores == nullptr || st == nullptr) return fail(FAS_ERR_INVALID, fn, "scores is NULL");
+  if (st[3] != 1) return fail(FAS_ERR_INVALID, fn, "scores innermost stride must be 1");
+  if (reinterpret_cast<uintptr_t>(scores) & 1u)
+    return fail(FAS_ERR_INVALID, fn, "scores is not 2-byte aligned");
+  if ((int64_t)fas::kFwdRows * st[2] * 2 >= kMaxSliceBytes)
+    return fail(FAS_ERR_UNSUPPORTED, fn, "score rows too long for 32-bit offsets");
+  return FAS_OK;
+}
+
+// Scores alone through the scores-only kernel; mask selects the causal /
+// key-range mask with masked entries written as 0.
+static int run_scores(const char* fn, const fas_attn_args* a, const Problem& pr, void* scores,
+               const int64_t* st, bool mask, void* stream) {
+  fas::ScoresParams p{};
+  p.q = static_cast<const uint16_t*>(a->q);
+  p.k = static_cast<const uint16_t*>(a->k);
+  p.scores = static_cast<uint16_t*>(scores);
+  p.sq0 = a->q_stride[0]; p.sq1 = a->q_stride[1]; p.sq2 = a->q_stride[2];
+  p.sk0 = a->k_stride[0]; p.sk1 = a->k_stride[1]; p.sk2 = a->k_stride[2];
+  p.ss0 = st[0]; p.ss1 = st[1]; p.ss2 = st[2];
+  p.q_bytes = slice_bytes(pr.M, p.sq2, pr.D);
+  p.k_bytes = slice_bytes(pr.N, p.sk2, pr.D);
+  p.B = pr.B; p.H = pr.H; p.G = pr.G; p.M = pr.M; p.N = pr.N;
+  p.mask = mask && pr.causal ? 1 : 0;
+  p.causal_off = pr.N - pr.M;
+  p.nrb = (pr.M + 31) / 32;
+  p.nkb = (pr.N + 511) / 512;
+  p.vec = aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 ? 1 : 0;
+  p.sm_scale = pr.sm_scale;
+  return hip_status(fn, fas::launch_scores(p, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
+}
+
+static int attention_with_scores_impl(const fas_attn_args* a, void* scores, const int64_t st[4],
+                                   void* ws, size_t ws_bytes, void* stream) {
   static const char* fn = "fas_attention_with_scores";
   Problem pr;
   int rc;
   if ((rc = check_args(fn, a, &pr))) return rc;
   if ((int64_t)pr.B * pr.H * pr.M == 0) return FAS_OK;
-  if (scores == nullptr || st == nullptr) return fail(FAS_ERR_INVALID, fn, "scores is NULL");
-  if (st[3] != 1) return fail(FAS_ERR_INVALID, fn, "scores innermost stride must be 1");
-  if (reinterpret_cast<uintptr_t>(scores) & 1u)
-    return fail(FAS_ERR_INVALID, fn, "scores is not 2-byte aligned");
+  if ((rc = check_scores_out(fn, scores, st))) return rc;
+  const Workspace w = layout(FAS_VARIANT_SCORES, pr, 0);
+  if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
+  if (w.has_split) {
+    // Short query range: the fused writer would run one workgroup per row
+    // block for every key tile; the key-split plain forward gives O and the
+    // scores-only kernel writes the masked scores in parallel over keys.
+    fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
+    apply_split(p, pr, w, ws, false);
+    if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, stream))) return rc;
+    return run_scores(fn, a, pr, scores, st, true, stream);
+  }
   const int bm = fas::kFwdRows;
-  if ((int64_t)bm * st[2] * 2 >= kMaxSliceBytes)
-    return fail(FAS_ERR_UNSUPPORTED, fn, "score rows too long for 32-bit offsets");
   fas::FwdParams p = fwd_params(a, pr, false, bm);
   p.scores = static_cast<uint16_t*>(scores);
   p.ss0 = st[0];
@@ -488,6 +529,24 @@ int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_
   p.vec_scores =
       aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && pr.N % 8 == 0;
   return run_fwd(fn, p, pr, fas::kFwdScores, stream);
+}
+
+int fas_attention_with_scores(const fas_attn_args* a, void* scores, const int64_t st[4], void* ws,
+                              size_t ws_bytes, void* stream) {
+  return attention_with_scores_impl(a, scores, st, ws, ws_bytes, stream);
+}
+
+int fas_attention_scores(const fas_attn_args* a, void* scores, const int64_t st[4],
+                         void* stream) {
+  static const char* fn = "fas_attention_scores";
+  Problem pr;
+  int rc;
+  if ((rc = check_shape(fn, a, &pr))) return rc;
+  if ((int64_t)pr.B * pr.H * pr.M * pr.N == 0) return FAS_OK;
+  if ((rc = check_tensor(fn, "q", a->q, a->q_stride, pr.M, pr.D))) return rc;
+  if ((rc = check_tensor(fn, "k", a->k, a->k_stride, pr.N, pr.D))) return rc;
+  if ((rc = check_scores_out(fn, scores, st))) return rc;
+  return run_scores(fn, a, pr, scores, st, false, stream);
 }
 
 int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum, const int64_t st[3],

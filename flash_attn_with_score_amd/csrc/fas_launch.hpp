@@ -25,6 +25,9 @@ hipError_t launch_bwd(const BwdParams& p, int dtype, int d, hipStream_t s);
 // Rows per dK/dV key block and per dQ row block of the backward kernels.
 constexpr int kBwdBlock = 128;
 
+// Scores alone, (q . k) * sm_scale, optionally masked (fas_scores.hpp).
+hipError_t launch_scores(const ScoresParams& p, int dtype, int d, hipStream_t s);
+
 hipError_t launch_fill_zero(float* p, int64_t s0, int64_t s1, int64_t s2, int64_t n0, int64_t n1,
                             int64_t n2, hipStream_t s);
 

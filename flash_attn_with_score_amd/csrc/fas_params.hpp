@@ -134,3 +134,25 @@ struct BwdParams {
 };
 
 }  // namespace fas
+
+namespace fas {
+
+// Scores alone (fas_scores.hpp): (q . k) * sm_scale in the input dtype.
+struct ScoresParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  uint16_t* scores;
+  int64_t sq0, sq1, sq2;
+  int64_t sk0, sk1, sk2;
+  int64_t ss0, ss1, ss2;
+  uint32_t q_bytes, k_bytes;
+  int B, H, G, M, N;
+  int mask;           // 1: causal / key-range mask, masked entries written as 0
+  int causal_off;     // key j admissible for query i iff causal_off + i >= j
+  int nrb;            // 32-row blocks
+  int nkb;            // 512-key blocks
+  int vec;            // rows 16-byte aligned and N % 8 == 0: 16-byte stores
+  float sm_scale;     // signed
+};
+
+}  // namespace fas

@@ -109,9 +109,20 @@ size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split);
 /* Replaces attention_with_scores.py:214-333 (+ _fwd_kernel_with_scores
  * :23-211).  scores is (B, Hq, M, N) in the input dtype with element strides
  * scores_stride (innermost 1); it receives (q.k) * sm_scale, with masked
- * positions (causal, upper triangle) written as 0 by the kernel itself. */
+ * positions (causal, upper triangle) written as 0 by the kernel itself.
+ * Workspace: fas_workspace_bytes(FAS_VARIANT_SCORES, ...), non-zero only
+ * for short query ranges, which run the key-split forward plus the
+ * scores-only kernel instead of the fused writer. */
 int fas_attention_with_scores(const fas_attn_args* a, void* scores,
-                              const int64_t scores_stride[4], void* stream);
+                              const int64_t scores_stride[4], void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Replaces attention_scores.py:154-223 (compute_attention_scores + kernel
+ * :55-151): scores (B, Hq, M, N) in the input dtype receives
+ * (q . k) * sm_scale for every pair, with no mask (the reference ignores
+ * causal there).  Only a->q and a->k are read. */
+int fas_attention_scores(const fas_attn_args* a, void* scores, const int64_t scores_stride[4],
+                         void* stream);
 
 /* Replaces attention_with_row_sum.py:204-326 (+ kernel :22-202).
  * row_sum is (B, Hq, M) fp32: sum over admissible keys of (q.k)*sm_scale.

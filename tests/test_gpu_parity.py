@@ -96,7 +96,7 @@ SPLIT_SHAPES = [
 
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("shape", SPLIT_SHAPES, ids=_label)
-@pytest.mark.parametrize("ep", [e for e in PLAIN_EPS if e != "attention_with_scores"] + [
+@pytest.mark.parametrize("ep", PLAIN_EPS + [
     "attention_cross_token_qk_sum", "attention_cross_token_softmax_sum"])
 def test_key_split_forward(ep, shape, causal, gpu):
     split = None
@@ -193,3 +193,22 @@ def test_repeat_calls_consistent(gpu):
     _, a = fas.attention_with_softmax_col_sum(q, k, v, causal=True)
     _, b = fas.attention_with_softmax_col_sum(q, k, v, causal=True)
     assert_sum_close(a, b, "repeat")
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 2, 96, 200, 64), (2, 2, 1, 33, 1000, 128),
+                                   (1, 3, 3, 300, 70, 16), (1, 2, 2, 64, 64, 32)], ids=_label)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_compute_attention_scores(shape, dtype, gpu):
+    """attention_scores.compute_attention_scores: unmasked (q . k) * sm_scale
+    for every pair, causal accepted and ignored (attention_scores.py:154-223)."""
+    from flash_attn_with_score_amd.attention_scores import compute_attention_scores
+
+    B, Hq, Hk, M, N, D = shape
+    print(f"[case] compute_attention_scores {_label(shape)} {dtype}", flush=True)
+    q, k, _ = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=4)
+    got = compute_attention_scores(q.to(gpu), k.to(gpu), causal=True)
+    torch.cuda.synchronize()
+    ref = naive.reference_forward(q, k, k, causal=False, want=("scores",))["scores"]
+    assert got.dtype == dtype and got.shape == (B, Hq, M, N)
+    assert_out_close(got, ref, "scores")
+

@@ -154,7 +154,7 @@ def test_key_split_workspace(lib):
     assert ws(_native.VARIANT_ATTENTION_FORWARD) == split
     assert ws(_native.VARIANT_SOFTMAX_COL_SUM) == (
         r256(B * Hq * M * 4) + r256(B * Hq * N * 4) + split)
-    assert ws(_native.VARIANT_SCORES) == 0  # the score writer never splits
+    assert ws(_native.VARIANT_SCORES) == split  # key-split forward + scores-only kernel
     # enough row blocks: no split
     a = make_args(1, 32, 32, 4096, 4096, 128)
     assert lib.fas_workspace_bytes(_native.VARIANT_ROW_SUM, ctypes.byref(a), 0) == 0
@@ -176,7 +176,7 @@ def _err(lib):
 def test_rejects_unsupported_head_dim(lib):
     a = make_args(D=48)
     st = _native._I64x4(1, 1, 1, 1)
-    rc = lib.fas_attention_with_scores(ctypes.byref(a), 0x10000, st, None)
+    rc = lib.fas_attention_with_scores(ctypes.byref(a), 0x10000, st, None, 0, None)
     assert rc == _native.FAS_ERR_UNSUPPORTED
     assert "fas_attention_with_scores" in _err(lib) and "head_dim 48" in _err(lib)
 
