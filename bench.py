@@ -56,6 +56,9 @@ WORKLOADS = {
     # attention()'s backward pass alone (flash.py:172-261), FA2 convention:
     # 2.5x the forward's 4*B*H*D*P.
     "attention_bwd": ("attention", False, "mfma", 10),
+    # attention_scores.compute_attention_scores (attention_scores.py:154-223):
+    # the unmasked score matrix alone, 2*B*H*M*N*D FLOP.
+    "scores_only": ("compute_attention_scores", False, "hbm", 2),
 }
 
 
@@ -86,6 +89,10 @@ def work(name: str, B, H, Hk, M, N, D, causal, split, elem=2):
     qkvo = elem * (2 * B * H * M * D + 2 * B * Hk * N * D)
     if name == "scores":
         return 4 * B * H * D * P, qkvo + elem * B * H * M * N
+    if name == "scores_only":
+        # reads q, k; writes the full score matrix
+        return (fac * B * H * M * N * D,
+                elem * (B * H * M * D + B * Hk * N * D + B * H * M * N))
     if name == "row_sum":
         return 4 * B * H * D * P, qkvo + 4 * B * H * M
     if name in ("col_sum", "col_sum_sequential", "col_softmax"):
@@ -182,6 +189,9 @@ def make_call(fas, name, q, k, v, causal, split):
         g = torch.Generator(device=q.device).manual_seed(1)
         do = torch.randn(o.shape, generator=g, device=q.device, dtype=o.dtype)
         return lambda: torch.autograd.grad(o, (qg, kg, vg), do, retain_graph=True)
+    if name == "scores_only":
+        from flash_attn_with_score_amd.attention_scores import compute_attention_scores
+        return lambda: compute_attention_scores(q, k)
     fn = getattr(fas, WORKLOADS[name][0])
     if WORKLOADS[name][1]:
         return lambda: fn(q, k, v, split, causal=causal)
@@ -327,7 +337,7 @@ def main() -> int:
 
     del q, k, v
     torch.cuda.synchronize()
-    if args.cpu_budget > 0 and args.workload != "attention_bwd":
+    if args.cpu_budget > 0 and args.workload not in ("attention_bwd", "scores_only"):
         line["cpu_baseline"] = cpu_baseline(args.workload, B, H, Hk, M, N, D, causal, split,
                                             dtype, args.cpu_budget)
     else:

@@ -184,23 +184,26 @@ struct Workspace {
 // Key split of the plain / row-sum forward.  When the row blocks of the
 // whole problem give fewer workgroups than the chip has CUs (short query
 // ranges against long key ranges: decode, last-window scoring), each row
-// block's key tiles are dealt to nsplit workgroups of at least 4 tiles,
+// block's key tiles are dealt to nsplit workgroups of at least 8 tiles,
 // aiming at ~512 workgroups in all.  Depends on sizes only, so the workspace
-// query and the launch agree.
+// query and the launch agree.  The scores variant splits only below 64 row
+// blocks: its split route writes the scores in a second kernel, which the
+// fused writer beats while it still has a quarter of the CUs busy.
 struct SplitPlan {
   int nsplit = 1, tps = 0;
   int64_t mpad = 0;
 };
-SplitPlan split_plan(const Problem& pr, bool top_left) {
+constexpr int64_t kScoresSplitMaxWgs = 64;
+SplitPlan split_plan(const Problem& pr, bool top_left, int64_t max_wgs = 255) {
   SplitPlan sp;
   const int64_t nrb = ((int64_t)pr.M + fas::kFwdRows - 1) / fas::kFwdRows;
   const int64_t wgs = (int64_t)pr.B * pr.H * nrb;
-  if (wgs == 0 || wgs >= 256) return sp;
+  if (wgs == 0 || wgs > max_wgs) return sp;
   const int64_t off = top_left ? 0 : (int64_t)pr.N - pr.M;
   int64_t hi = pr.N;
   if (pr.causal) hi = std::min<int64_t>(pr.N, std::max<int64_t>(0, off + nrb * fas::kFwdRows));
   const int64_t nt = (hi + 63) / 64;
-  int64_t ns = std::min<int64_t>((512 + wgs - 1) / wgs, nt / 4);
+  int64_t ns = std::min<int64_t>((512 + wgs - 1) / wgs, nt / 8);
   if (ns < 2) return sp;
   const int64_t tps = (nt + ns - 1) / ns;
   ns = (nt + tps - 1) / tps;
@@ -280,7 +283,8 @@ Workspace layout(int variant, const Problem& pr, int64_t split) {
     }
   }
   if (forward_can_split(variant)) {
-    const SplitPlan sp = split_plan(pr, variant == FAS_VARIANT_CROSS_QK_SUM);
+    const SplitPlan sp = split_plan(pr, variant == FAS_VARIANT_CROSS_QK_SUM,
+                                    variant == FAS_VARIANT_SCORES ? kScoresSplitMaxWgs : 255);
     if (sp.nsplit > 1) {
       const size_t rows = (size_t)pr.B * pr.H * sp.nsplit * sp.mpad;
       w.has_split = true;
@@ -494,9 +498,12 @@ static int run_scores(const char* fn, const fas_attn_args* a, const Problem& pr,
   p.B = pr.B; p.H = pr.H; p.G = pr.G; p.M = pr.M; p.N = pr.N;
   p.mask = mask && pr.causal ? 1 : 0;
   p.causal_off = pr.N - pr.M;
-  p.nrb = (pr.M + 31) / 32;
-  p.nkb = (pr.N + 511) / 512;
-  p.vec = aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 ? 1 : 0;
+  p.nrb = (pr.M + 255) / 256;
+  p.nkb = (pr.N + 127) / 128;
+  p.vec = aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 &&
+                  pr.N % 8 == 0
+              ? 1
+              : 0;
   p.sm_scale = pr.sm_scale;
   return hip_status(fn, fas::launch_scores(p, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
 }

@@ -40,29 +40,6 @@ namespace fas {
 
 constexpr float kLog2e = 1.44269504088896341f;
 
-// LDS DMA of rows [r0, r0 + R) of a row-major (., D) 16-bit matrix into a
-// swizzled R x D LDS tile at byte address lds: 1 KiB blocks dealt to the NW
-// waves; lane l fills physical chunk l % (D/8) of its row, i.e. logical
-// chunk (l % (D/8)) ^ swz(row).  Rows outside the buffer read as zeros.
-template <int D, int R, int NW>
-__device__ __forceinline__ void dma_tile(i32x4 rsrc, int64_t stride, int r0, uint32_t lds,
-                                         int wave, int lane) {
-  constexpr int BLOCKS = R * D / 512;
-  constexpr int RPB = 512 / D;
-  constexpr int CPR = D / 8;
-  constexpr int PER = (BLOCKS + NW - 1) / NW;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int q = wave + i * NW;
-    if (BLOCKS % NW == 0 || q < BLOCKS) {
-      const int row = q * RPB + lane / CPR;
-      const int ch = (lane % CPR) ^ swz<D>(row);
-      dma16(rsrc, (uint32_t)(((r0 + row) * stride + ch * 8) * 2),
-            __builtin_amdgcn_readfirstlane(lds + (uint32_t)(q * 1024)));
-    }
-  }
-}
-
 // Packs accumulator registers 8cs..8cs+7 (contraction indices 8g..8g+7 of
 // k-step cs) as an MFMA B operand.
 template <class E>

@@ -149,9 +149,9 @@ struct ScoresParams {
   int B, H, G, M, N;
   int mask;           // 1: causal / key-range mask, masked entries written as 0
   int causal_off;     // key j admissible for query i iff causal_off + i >= j
-  int nrb;            // 32-row blocks
-  int nkb;            // 512-key blocks
-  int vec;            // rows 16-byte aligned and N % 8 == 0: 16-byte stores
+  int nrb;            // 256-row blocks
+  int nkb;            // 128-key blocks
+  int vec;            // base and row strides 16-byte aligned, N % 8 == 0: 16-byte stores
   float sm_scale;     // signed
 };
 

@@ -7,7 +7,9 @@ namespace fas {
 template <class E, int D>
 static hipError_t scores_t(const ScoresParams& p, hipStream_t s) {
   const int64_t grid = (int64_t)p.B * p.H * p.nrb * p.nkb;
-  if (grid > 0) hipLaunchKernelGGL((scores_kernel<E, D>), dim3((unsigned)grid), dim3(256), 0, s, p);
+  if (grid > INT32_MAX) return hipErrorInvalidValue;
+  if (grid > 0)
+    hipLaunchKernelGGL((scores_kernel<E, D>), dim3((unsigned)grid), dim3(64 * kScoresWaves), 0, s, p);
   return hipGetLastError();
 }
 

@@ -196,7 +196,9 @@ def test_repeat_calls_consistent(gpu):
 
 
 @pytest.mark.parametrize("shape", [(1, 4, 2, 96, 200, 64), (2, 2, 1, 33, 1000, 128),
-                                   (1, 3, 3, 300, 70, 16), (1, 2, 2, 64, 64, 32)], ids=_label)
+                                   (1, 3, 3, 300, 70, 16), (1, 2, 2, 64, 64, 32),
+                                   (1, 2, 2, 600, 520, 128), (1, 2, 1, 513, 1029, 64)],
+                         ids=_label)
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 def test_compute_attention_scores(shape, dtype, gpu):
     """attention_scores.compute_attention_scores: unmasked (q . k) * sm_scale

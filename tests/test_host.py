@@ -141,13 +141,13 @@ def test_attention_entry_points_reject_bad_requests(lib):
 
 def test_key_split_workspace(lib):
     """Short query range against long keys: B*Hq*ceil(M/256) = 4 workgroups,
-    32 key tiles -> 8 splits of 4 tiles; partials (B*Hq*8*256) x (D + 3) fp32."""
+    32 key tiles -> 4 splits of 8 tiles; partials (B*Hq*4*256) x (D + 3) fp32."""
     def r256(x):
         return (x + 255) // 256 * 256
 
     B, Hq, Hk, M, N, D = 1, 4, 2, 32, 2048, 128
     a = make_args(B, Hq, Hk, M, N, D)
-    rows = B * Hq * 8 * 256
+    rows = B * Hq * 4 * 256
     split = r256(rows * D * 4) + 3 * r256(rows * 4)
     ws = lambda v, s=0: lib.fas_workspace_bytes(v, ctypes.byref(a), s)  # noqa: E731
     assert ws(_native.VARIANT_ROW_SUM) == split
