@@ -51,9 +51,8 @@ class Problem:
 
 def check_device_inputs(q, k, v, dropout_p: float) -> None:
     """Checks this build adds after the reference's own asserts."""
-    if dropout_p > 0.0:
-        raise NotImplementedError(
-            "flash_attn_with_score_amd: dropout_p > 0 is not supported by the gfx950 kernels")
+    if not 0.0 <= dropout_p < 1.0:
+        raise ValueError(f"flash_attn_with_score_amd: dropout_p {dropout_p} outside [0, 1)")
     assert q.dtype in _native.DTYPE_CODES, f"q.dtype must be float16 or bfloat16, got {q.dtype}"
     assert k.dtype == q.dtype and v.dtype == q.dtype, "q, k, v must share one dtype"
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
@@ -62,6 +61,20 @@ def check_device_inputs(q, k, v, dropout_p: float) -> None:
     assert q.dim() == 4 and k.dim() == 4 and v.dim() == 4, "q, k, v must be (B, H, S, D)"
     assert k.shape[0] == q.shape[0] and v.shape[0] == q.shape[0], "batch sizes must match"
     assert v.shape[2] == k.shape[2], "k and v must have the same sequence length"
+
+
+def draw_dropout(q, k, dropout_p: float):
+    """(dropout_p, seed, offset) for a launcher that applies dropout, drawn as
+    the reference's launchers draw it: philox_cuda_seed_offset(B*H*M*N)
+    before the launch (e.g. attention_with_scores.py:264-268); None when
+    dropout_p is 0."""
+    if not dropout_p > 0.0:
+        return None
+    from .dropout import philox_cuda_seed_offset
+
+    B, H, M, _ = q.shape
+    seed, offset = philox_cuda_seed_offset(B * H * M * k.shape[2], q.device.index)
+    return (dropout_p, seed, offset)
 
 
 def finish_problem(q, k, v, sm_scale) -> Problem:

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -61,6 +61,10 @@ class AttnArgs(ctypes.Structure):
         ("k_stride", _I64x4),
         ("v_stride", _I64x4),
         ("out_stride", _I64x4),
+        ("dropout_p", ctypes.c_float),
+        ("reserved2", ctypes.c_int32),
+        ("dropout_seed", ctypes.c_uint64),
+        ("dropout_offset", ctypes.c_uint64),
     ]
 
 
@@ -72,7 +76,8 @@ def strides3(t: torch.Tensor):
     return _I64x3(*t.stride())
 
 
-def make_args(q, k, v, o, causal: bool, sm_scale: float) -> AttnArgs:
+def make_args(q, k, v, o, causal: bool, sm_scale: float, dropout=None) -> AttnArgs:
+    """dropout: None, or (dropout_p, seed, offset) of the reference's stream."""
     B, H, M, D = q.shape
     a = AttnArgs()
     a.dtype = DTYPE_CODES[q.dtype]
@@ -83,6 +88,10 @@ def make_args(q, k, v, o, causal: bool, sm_scale: float) -> AttnArgs:
     a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
     a.q_stride, a.k_stride, a.v_stride, a.out_stride = (
         strides4(q), strides4(k), strides4(v), strides4(o))
+    if dropout is not None:
+        a.dropout_p = float(dropout[0])
+        a.dropout_seed = int(dropout[1]) & 0xFFFFFFFFFFFFFFFF
+        a.dropout_offset = int(dropout[2]) & 0xFFFFFFFFFFFFFFFF
     return a
 
 

@@ -71,7 +71,8 @@ def attention_cross_token_qk_sum(
     # A caller buffer the kernel cannot write directly (innermost stride != 1
     # or unaligned rows) is filled through a temporary.
     o_k = o if (o.stride(-1) == 1 and _common._rows_aligned(o)) else _common.new_output(p.q)
-    args = _native.make_args(p.q, p.k, p.v, o_k, causal, p.sm_scale)
+    args = _native.make_args(p.q, p.k, p.v, o_k, causal, p.sm_scale,
+                             _common.draw_dropout(p.q, p.k, dropout_p))
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_CROSS_QK_SUM, args, split, q.device)
     _common.call("fas_attention_cross_token_qk_sum", p.q, ctypes.byref(args), int(split),
                  cross_token_qk.data_ptr(), _native.strides3(cross_token_qk), ws_ptr, ws_bytes)

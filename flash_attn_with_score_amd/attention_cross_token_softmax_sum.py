@@ -49,6 +49,7 @@ def attention_cross_token_softmax_sum_buffered(
     p = _common.finish_problem(q, k, v, sm_scale)
     output = _common.new_output(p.q)
     cross = torch.empty((B, Hk, split), device=q.device, dtype=torch.float32)
+    # The reference's buffered kernel ignores dropout_p and draws no seed.
     args = _native.make_args(p.q, p.k, p.v, output, causal, p.sm_scale)
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_CROSS_SOFTMAX_SUM_BUFFERED, args, split,
                                              q.device)
@@ -86,7 +87,8 @@ def attention_cross_token_softmax_sum(
     p = _common.finish_problem(q, k, v, sm_scale)
     output = _common.new_output(p.q)
     cross = torch.empty((B, Hk, split), device=q.device, dtype=torch.float32)
-    args = _native.make_args(p.q, p.k, p.v, output, causal, p.sm_scale)
+    args = _native.make_args(p.q, p.k, p.v, output, causal, p.sm_scale,
+                             _common.draw_dropout(p.q, p.k, dropout_p))
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_CROSS_SOFTMAX_SUM, args, split,
                                              q.device)
     _common.call("fas_attention_cross_token_softmax_sum", p.q, ctypes.byref(args), int(split),

@@ -40,7 +40,8 @@ def attention_with_softmax_col_sum(
     p = _common.finish_problem(q, k, v, sm_scale)
     o = _common.new_output(p.q)
     col_sum = torch.empty((B, Hk, N), device=q.device, dtype=torch.float32)
-    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale,
+                             _common.draw_dropout(p.q, p.k, dropout_p))
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_SOFTMAX_COL_SUM, args, 0, q.device)
     _common.call("fas_attention_with_softmax_col_sum", p.q, ctypes.byref(args), col_sum.data_ptr(),
                  _native.strides3(col_sum), ws_ptr, ws_bytes)

@@ -38,7 +38,8 @@ def attention_with_row_sum(
     # Every element is written by the kernels (rows with no admissible key get
     # 0, attention_with_row_sum.py:185), so no zero-fill is needed.
     row_sum = torch.empty((B, H, M), device=q.device, dtype=torch.float32)
-    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale,
+                             _common.draw_dropout(p.q, p.k, dropout_p))
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ROW_SUM, args, 0, q.device)
     _common.call("fas_attention_with_row_sum", p.q, ctypes.byref(args), row_sum.data_ptr(),
                  _native.strides3(row_sum), ws_ptr, ws_bytes)

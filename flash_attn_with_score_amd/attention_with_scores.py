@@ -42,7 +42,8 @@ def attention_with_scores(
     p = _common.finish_problem(q, k, v, sm_scale)
     o = _common.new_output(p.q)
     scores = torch.empty((B, H, M, N), device=q.device, dtype=q.dtype)
-    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale,
+                             _common.draw_dropout(p.q, p.k, dropout_p))
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_SCORES, args, 0, q.device)
     _common.call("fas_attention_with_scores", p.q, ctypes.byref(args), scores.data_ptr(),
                  _native.strides4(scores), ws_ptr, ws_bytes)

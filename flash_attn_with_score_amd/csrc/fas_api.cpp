@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -83,6 +84,13 @@ int check_shape(const char* fn, const fas_attn_args* a, Problem* pr) {
   if (a->seqlen_q > (1 << 28) || a->seqlen_k > (1 << 28) || a->batch * a->heads_q > (1 << 24))
     return fail(FAS_ERR_UNSUPPORTED, fn, "sizes exceed the index range of the kernels");
   if (!std::isfinite(a->sm_scale)) return fail(FAS_ERR_INVALID, fn, "sm_scale is not finite");
+  if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f))
+    return fail(FAS_ERR_INVALID, fn, "dropout_p %g outside [0, 1)", (double)a->dropout_p);
+  if (a->dropout_p > 0.f && a->dropout_offset >= (1ull << 31) &&
+      (uint64_t)a->batch * a->heads_q * a->seqlen_q * a->seqlen_k >= (1ull << 31))
+    return fail(FAS_ERR_UNSUPPORTED, fn,
+                "dropout offset >= 2^31 with B*Hq*M*N >= 2^31 (the reference's element "
+                "index then depends on its block sizes)");
   pr->B = (int)a->batch;
   pr->H = (int)a->heads_q;
   pr->Hk = (int)a->heads_k;
@@ -121,6 +129,42 @@ float qk_scale_of(float sm_scale) {
   return (float)((double)std::fabs(sm_scale) * 1.4426950408889634);
 }
 
+// Dropout threshold: the largest y in [0, 2^31 - 1] whose uniform
+// float(y) * 4.6566127342e-10 (Triton's uint_to_uniform_float, fp32) is
+// <= p, so that "u > p" is "y > thresh".  u is non-decreasing in y.
+int32_t dropout_thresh(float p) {
+  auto u = [](int64_t y) { return (float)y * 4.6566127342e-10f; };
+  int64_t lo = 0, hi = INT32_MAX;  // u(lo) <= p
+  if (u(hi) <= p) return INT32_MAX;
+  while (hi - lo > 1) {
+    const int64_t mid = lo + (hi - lo) / 2;
+    if (u(mid) <= p)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  return (int32_t)lo;
+}
+
+fas::DropParams drop_params(const fas_attn_args* a, const Problem& pr) {
+  fas::DropParams d{};
+  d.scale = 1.f;
+  if (!(a->dropout_p > 0.f)) return d;
+  d.offset = a->dropout_offset;
+  d.k0 = (uint32_t)a->dropout_seed;
+  d.k1 = (uint32_t)(a->dropout_seed >> 32);
+  d.thresh = dropout_thresh(a->dropout_p);
+  d.wide = a->dropout_offset >= (1ull << 31) ? 1 : 0;
+  d.n = pr.N;
+  return d;
+}
+
+// O multiplier of the entry points that rescale kept weights (the reference
+// computes 1.0 / (1.0 - dropout_p) in fp32, attention_with_scores.py:200-203).
+void rescale_dropout(fas::FwdParams& p, const fas_attn_args* a) {
+  if (p.dropout) p.drop.scale = 1.f / (1.f - a->dropout_p);
+}
+
 // Fills the forward parameter block.  top_left selects the cross-token
 // QK-sum's causal alignment (i >= j) instead of (N - M) + i >= j.
 fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_left, int rows_per_block) {
@@ -149,6 +193,8 @@ fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_le
   p.nsplit = 1;
   p.sm_scale = std::fabs(pr.sm_scale);
   p.qk_scale = qk_scale_of(pr.sm_scale);
+  p.dropout = a->dropout_p > 0.f ? 1 : 0;
+  p.drop = drop_params(a, pr);
   return p;
 }
 
@@ -433,6 +479,10 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   c.causal_off = pr.N - pr.M;
   c.nkb = (int)((ncols + 255) / 256);
   c.qk_scale = p.qk_scale;
+  // Only the softmax column sum masks its weights; the cross-token pass
+  // does not (attention_cross_token_softmax_sum.py has no dropout there).
+  c.dropout = variant == FAS_VARIANT_SOFTMAX_COL_SUM ? p.dropout : 0;
+  c.drop = p.drop;
   float* part = nullptr;
   if (pr.G > 1) {
     part = at<float>(ws, w.part);
@@ -523,12 +573,14 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
     // block for every key tile; the key-split plain forward gives O and the
     // scores-only kernel writes the masked scores in parallel over keys.
     fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
+    rescale_dropout(p, a);
     apply_split(p, pr, w, ws, false);
     if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, stream))) return rc;
     return run_scores(fn, a, pr, scores, st, true, stream);
   }
   const int bm = fas::kFwdRows;
   fas::FwdParams p = fwd_params(a, pr, false, bm);
+  rescale_dropout(p, a);
   p.scores = static_cast<uint16_t*>(scores);
   p.ss0 = st[0];
   p.ss1 = st[1];
@@ -626,6 +678,7 @@ int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3
   const Workspace w = layout(FAS_VARIANT_ATTENTION_FORWARD, pr, 0);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
+  rescale_dropout(p, a);
   apply_split(p, pr, w, ws, false);
   p.lse_ln = lse;
   p.sl0 = st[0];
@@ -677,6 +730,8 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   Problem pr;
   int rc;
   if ((rc = check_args(fn, a, &pr))) return rc;
+  if (a->dropout_p > 0.f)
+    return fail(FAS_ERR_UNSUPPORTED, fn, "the backward pass with dropout_p > 0 is not implemented");
   if ((int64_t)pr.B * pr.H == 0) return FAS_OK;
   if (pr.M > 0) {
     if (gst == nullptr || qst == nullptr || lst == nullptr || lse == nullptr)

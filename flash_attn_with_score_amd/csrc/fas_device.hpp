@@ -175,6 +175,43 @@ __device__ __forceinline__ void buf_store16_nt(u32x4 v, __amdgpu_buffer_rsrc_t r
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, soff, kAuxNT);
 }
 
+// Philox4x32 with 6 rounds on counter (c0, c1, 0, 0) and key (k0, k1): the
+// first output word, i.e. Triton's randint(seed, offset, n_rounds=6)
+// (triton/language/random.py: philox_impl, randint4x), which follows the
+// Random123 Philox round: multipliers 0xD2511F53 / 0xCD9E8D57, key
+// increments 0x9E3779B9 / 0xBB67AE85 (Salmon et al., SC'11).  Each 32x32
+// product is one 64-bit multiply giving both halves; the unused parts of
+// the first and last rounds fold away.
+__device__ __forceinline__ uint32_t philox6_word0(uint32_t c0, uint32_t c1, uint32_t k0,
+                                                  uint32_t k1) {
+  uint32_t c2 = 0, c3 = 0;
+#pragma unroll
+  for (int r = 0; r < 6; ++r) {
+    const uint64_t pa = (uint64_t)0xD2511F53u * c0;
+    const uint64_t pb = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(pb >> 32) ^ c1 ^ k0;
+    const uint32_t n2 = (uint32_t)(pa >> 32) ^ c3 ^ k1;
+    c1 = (uint32_t)pb;
+    c3 = (uint32_t)pa;
+    c0 = n0;
+    c2 = n2;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c0;
+}
+// Dropout keep decision for element index idx (mod 2^32).  Triton's uniform
+// is u = float(y) * 4.6566127342e-10 with y = x for x >= 0, -x - 1 (= ~x)
+// otherwise (x the random word as int32), and it keeps u > p.  u is
+// non-decreasing in y, so the host folds "u > p" into y > thresh.
+template <class DP>
+__device__ __forceinline__ bool dropout_keep(const DP& d, uint32_t idx) {
+  const uint64_t ctr = d.offset + idx;
+  const uint32_t x = philox6_word0((uint32_t)ctr, d.wide ? (uint32_t)(ctr >> 32) : 0u, d.k0, d.k1);
+  const int32_t y = (int32_t)(x ^ (uint32_t)((int32_t)x >> 31));
+  return y > d.thresh;
+}
+
 // Row permutation applied to MFMA operand rows (bits 2 and 3 swapped).  With
 // it the 16 accumulator registers of lane l (g = l / 32) cover rows
 // {16*(r/8) + 8g + r%8}: two runs of 8 consecutive rows, so a lane's values

@@ -177,7 +177,7 @@ __device__ __forceinline__ void sched_score_tile() {
   if (NST > KS) __builtin_amdgcn_sched_group_barrier(0x040, NST > KS ? NST - KS : 1, 0);
 }
 
-template <class E, int D, int MODE, int NW>
+template <class E, int D, int MODE, int NW, bool DROP>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(const FwdParams p) {
   static_assert(MODE != kFwdScores || NW == 8, "the score writer uses 8 waves");
@@ -423,6 +423,21 @@ void fwd_kernel(const FwdParams p) {
     }
     return lt;
   };
+  // Dropout (DROP instances): zero the packed weights of dropped elements
+  // after the row sum has taken them (attention_with_scores.py:169-176).
+  // Weight e of pb[cs] is key k0 + 16cs + 8g + e of this lane's row.
+  const uint32_t drow = ((uint32_t)bh * (uint32_t)p.M + (uint32_t)qrow) * (uint32_t)p.drop.n;
+  auto drop_p = [&](u32x4 (&pb)[4], int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int cs = 0; cs < 4; ++cs)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t i0 = drow + (uint32_t)(k0 + 16 * cs + 8 * g + 2 * w);
+        const uint32_t m = (dropout_keep(p.drop, i0) ? 0xFFFFu : 0u) |
+                           (dropout_keep(p.drop, i0 + 1) ? 0xFFFF0000u : 0u);
+        pb[cs][w] &= m;
+      }
+  };
   auto pv_mma = [&](const u32x4 (&pb)[4], const uint16_t* vt) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -575,6 +590,7 @@ void fwd_kernel(const FwdParams p) {
           }
         }
         l_i += lt;
+        if constexpr (DROP) drop_p(pb, k0);
         if constexpr (ST) {
           // O += P V with zero slots in between.
           pv_mma(pb, vt);
@@ -674,7 +690,8 @@ void fwd_kernel(const FwdParams p) {
       return;
     }
   }
-  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if constexpr (DROP) inv *= p.drop.scale;
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.o + b * p.so0 + h * p.so1, p.o_bytes);
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -741,7 +758,7 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdParams p) {
     acc[4] = fmaf(w, x1.x, acc[4]); acc[5] = fmaf(w, x1.y, acc[5]);
     acc[6] = fmaf(w, x1.z, acc[6]); acc[7] = fmaf(w, x1.w, acc[7]);
   }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const float inv = l > 0.f ? p.drop.scale / l : 0.f;
   *reinterpret_cast<u32x4*>(p.o + b * p.so0 + h * p.so1 + (int64_t)row * p.so2 + 8 * ch) =
       u32x4{E::pack(acc[0] * inv, acc[1] * inv), E::pack(acc[2] * inv, acc[3] * inv),
             E::pack(acc[4] * inv, acc[5] * inv), E::pack(acc[6] * inv, acc[7] * inv)};
@@ -757,12 +774,12 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdParams p) {
   }
 }
 
-template <class E, int D, int MODE, int NW>
+template <class E, int D, int MODE, int NW, bool DROP>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdRowSum;
   const int64_t nsplit = kCanSplit ? p.nsplit : 1;
   const dim3 grid((unsigned)((int64_t)p.nrb * p.B * p.H * nsplit)), block(NW * 64);
-  hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW>), grid, block, 0, stream, p);
+  hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW, DROP>), grid, block, 0, stream, p);
   if constexpr (kCanSplit) {
     if (p.nsplit > 1 && p.M > 0) {
       const int64_t nblk = (p.M + 2048 / D - 1) / (2048 / D);
@@ -773,21 +790,21 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int MODE, int NW>
+template <int MODE, int NW, bool DROP = false>
 hipError_t launch_fwd_mode(const FwdParams& p, int dtype, int d, hipStream_t s) {
   if (dtype == 0) {
     switch (d) {
-      case 16: return launch_fwd_t<F16, 16, MODE, NW>(p, s);
-      case 32: return launch_fwd_t<F16, 32, MODE, NW>(p, s);
-      case 64: return launch_fwd_t<F16, 64, MODE, NW>(p, s);
-      case 128: return launch_fwd_t<F16, 128, MODE, NW>(p, s);
+      case 16: return launch_fwd_t<F16, 16, MODE, NW, DROP>(p, s);
+      case 32: return launch_fwd_t<F16, 32, MODE, NW, DROP>(p, s);
+      case 64: return launch_fwd_t<F16, 64, MODE, NW, DROP>(p, s);
+      case 128: return launch_fwd_t<F16, 128, MODE, NW, DROP>(p, s);
     }
   } else {
     switch (d) {
-      case 16: return launch_fwd_t<BF16, 16, MODE, NW>(p, s);
-      case 32: return launch_fwd_t<BF16, 32, MODE, NW>(p, s);
-      case 64: return launch_fwd_t<BF16, 64, MODE, NW>(p, s);
-      case 128: return launch_fwd_t<BF16, 128, MODE, NW>(p, s);
+      case 16: return launch_fwd_t<BF16, 16, MODE, NW, DROP>(p, s);
+      case 32: return launch_fwd_t<BF16, 32, MODE, NW, DROP>(p, s);
+      case 64: return launch_fwd_t<BF16, 64, MODE, NW, DROP>(p, s);
+      case 128: return launch_fwd_t<BF16, 128, MODE, NW, DROP>(p, s);
     }
   }
   return hipErrorInvalidValue;

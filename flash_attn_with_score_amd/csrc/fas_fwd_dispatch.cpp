@@ -7,8 +7,10 @@ hipError_t launch_fwd_plain(const FwdParams& p, int dtype, int d, hipStream_t s)
 hipError_t launch_fwd_rowsum(const FwdParams& p, int dtype, int d, hipStream_t s);
 hipError_t launch_fwd_scores(const FwdParams& p, int dtype, int d, hipStream_t s);
 hipError_t launch_fwd_region(const FwdParams& p, int dtype, int d, hipStream_t s);
+hipError_t launch_fwd_dropout(const FwdParams& p, int mode, int dtype, int d, hipStream_t s);
 
 hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, hipStream_t s) {
+  if (p.dropout && mode != kFwdRegion) return launch_fwd_dropout(p, mode, dtype, d, s);
   switch (mode) {
     case kFwdPlain: return launch_fwd_plain(p, dtype, d, s);
     case kFwdRowSum: return launch_fwd_rowsum(p, dtype, d, s);

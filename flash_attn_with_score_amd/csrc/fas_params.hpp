@@ -13,6 +13,20 @@ enum FwdMode : int {
   kFwdRegion = 3   // + fp32 raw scores of rows >= split, keys < split
 };
 
+// Dropout of the attention weights with the reference's random stream:
+// element (b, h, i, j) is kept iff Triton's tl.rand(seed, offset + ((b*H + h)
+// *M + i)*N + j, n_rounds=6) > p (attention_with_scores.py:70-75, 173-176).
+// The index is taken mod 2^32 (the reference's int32 arithmetic) and the
+// counter's high word is used only for offsets >= 2^31 (a 64-bit offset).
+struct DropParams {
+  uint64_t offset;  // Philox offset of element (0, 0, 0, 0)
+  uint32_t k0, k1;  // Philox key: the seed's low and high words
+  int32_t thresh;   // keep iff the folded random word (as int32) > thresh
+  int wide;         // 1: counter word 1 = high word of offset + index
+  int n;            // N of the element index
+  float scale;      // O multiplier: 1/(1-p) where the reference rescales, else 1
+};
+
 struct FwdParams {
   const uint16_t* q;
   const uint16_t* k;
@@ -38,6 +52,8 @@ struct FwdParams {
   int nrb;           // query row blocks
   int vec_scores;    // scores rows 16-byte aligned and N % 8 == 0
   int vec_region;    // split % 4 == 0
+  int dropout;       // 1: the dropout instances (modes other than kFwdRegion)
+  DropParams drop;   // scale also applies in the key-split combine (1 without dropout)
   // Split over keys (kFwdPlain, kFwdRowSum): nsplit workgroups per row block,
   // each taking tps key tiles and writing fp32 partials at row pitch Mpad
   // (= nrb * rows per workgroup); a combine pass merges them.
@@ -77,6 +93,8 @@ struct ColsmParams {
   int causal, causal_off;
   int nkb;               // key blocks
   float qk_scale;        // |sm_scale| * log2(e)
+  int dropout;           // 1: weights pass through the dropout mask
+  DropParams drop;
 };
 
 // Raw-score column sums by linearity: sum_i (q_i . k_j) = (sum_i q_i) . k_j.

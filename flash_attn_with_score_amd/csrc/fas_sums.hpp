@@ -56,7 +56,9 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
 // LN: the row offsets come from a natural-log normalizer (p.lse_ln,
 // total_attention) instead of the forward's base-2 LSE; a template flag so
 // the default copy carries no conversion code in its loop.
-template <class E, int D, bool LN>
+// DROP: the weights pass through the dropout mask before the sum, as the
+// reference's column pass does (attention_with_col_softmax_sum.py:237-244).
+template <class E, int D, bool LN, bool DROP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3, 4)))
 void colsm_kernel(const ColsmParams p) {
   constexpr int KS = D / 16;
@@ -207,6 +209,12 @@ void colsm_kernel(const ColsmParams p) {
             if constexpr (MASK) {
               const int row = r0 + 32 * qb + acc_row(r, g);
               if (p.causal_off + row < key0 + c) s[r] = 0.f;
+            }
+            if constexpr (DROP) {
+              const uint32_t row = (uint32_t)(r0 + 32 * qb + acc_row(r, g));
+              const uint32_t idx = ((uint32_t)bh * (uint32_t)p.M + row) * (uint32_t)p.drop.n +
+                                   (uint32_t)(key0 + c);
+              if (!dropout_keep(p.drop, idx)) s[r] = 0.f;
             }
           }
 #pragma unroll

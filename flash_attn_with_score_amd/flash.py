@@ -30,11 +30,12 @@ def _check_inputs(q, k, v):
     assert q.shape[1] % Hk == 0, "number of heads in q must be a multiple of that in k & v"
 
 
-def _forward(q, k, v, causal, sm_scale, want_total):
+def _forward(q, k, v, causal, sm_scale, want_total, dropout_p):
     p = _common.finish_problem(q, k, v, sm_scale)
     o = _common.new_output(p.q)
     L = torch.empty((p.B, p.H, p.M), device=q.device, dtype=torch.float32)
-    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale)
+    drop = _common.draw_dropout(p.q, p.k, dropout_p)
+    args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale, drop)
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_FORWARD, args, 0,
                                              q.device)
     _common.call("fas_attention_forward", p.q, ctypes.byref(args), L.data_ptr(),
@@ -44,30 +45,39 @@ def _forward(q, k, v, causal, sm_scale, want_total):
         tot = torch.empty((p.B, p.H, p.N), device=q.device, dtype=torch.float32)
         _common.call("fas_total_attention", p.q, ctypes.byref(args), L.data_ptr(),
                      _native.strides3(L), tot.data_ptr(), _native.strides3(tot))
-    return p, o, L, tot
+    return p, o, L, tot, drop
 
 
 class FlashAttention(torch.autograd.Function):
-    """flash.py:32-261 without dropout (dropout_p > 0 raises NotImplementedError)."""
+    """flash.py:32-261.  The forward applies dropout (flash.py:59-66, 459-466,
+    488-491); the backward of a forward with dropout_p > 0 raises
+    NotImplementedError."""
 
     @staticmethod
     def forward(ctx, q, k, v, causal, sm_scale, dropout_p, return_log_normalizer,
                 return_total_attention, return_seed_offset):
         _check_inputs(q, k, v)
         _common.check_device_inputs(q, k, v, dropout_p)
-        p, o, L, tot = _forward(q, k, v, causal, sm_scale, return_total_attention)
+        p, o, L, tot, drop = _forward(q, k, v, causal, sm_scale, return_total_attention,
+                                      dropout_p)
         ctx.save_for_backward(p.q, p.k, p.v, o, L)
         ctx.sm_scale = p.sm_scale
         ctx.causal = causal
+        ctx.dropout_p = dropout_p
         if return_log_normalizer or return_total_attention or return_seed_offset:
-            # Without dropout the reference returns None for seed and offset
+            # seed and offset only with dropout and return_seed_offset
             # (flash.py:161-169).
+            seed = drop[1] if drop is not None and return_seed_offset else None
+            offset = drop[2] if drop is not None and return_seed_offset else None
             return (o, L if return_log_normalizer else None,
-                    tot if return_total_attention else None, None, None)
+                    tot if return_total_attention else None, seed, offset)
         return o
 
     @staticmethod
     def backward(ctx, do, *ignored):
+        if ctx.dropout_p > 0.0:
+            raise NotImplementedError(
+                "flash_attn_with_score_amd: attention() backward with dropout_p > 0")
         q, k, v, o, L = ctx.saved_tensors
         B, H, M, D = q.shape
         Hk, N = k.shape[1], k.shape[2]

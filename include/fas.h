@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FAS_ABI_VERSION 4
+#define FAS_ABI_VERSION 5
 
 typedef enum fas_dtype {
   FAS_DTYPE_F16 = 0,
@@ -94,6 +94,24 @@ typedef struct fas_attn_args {
   int64_t k_stride[4];
   int64_t v_stride[4];
   int64_t out_stride[4];
+  /* Dropout of the attention weights, 0 <= dropout_p < 1 (0: none).  With
+   * the reference's random stream: element (b, h, i, j) is kept iff
+   * Triton's tl.rand(dropout_seed, dropout_offset + ((b*Hq + h)*M + i)*N
+   * + j, n_rounds=6) > dropout_p, the index taken mod 2^32
+   * (attention_with_scores.py:70-75, 173-176); seed and offset are the pair
+   * dropout.py:5-15 takes from the device generator.  Weights are dropped
+   * after the row normaliser has summed them.  Which outputs see the mask
+   * follows the reference entry point by entry point: O everywhere
+   * (rescaled by 1/(1 - dropout_p) only by fas_attention_with_scores and
+   * fas_attention_forward), the column sums of
+   * fas_attention_with_softmax_col_sum, nothing else.  The buffered cross
+   * softmax sum, the scores-only call, the total attention and the score and
+   * raw-sum outputs ignore it.  Offsets >= 2^31 with B*Hq*M*N >= 2^31 return
+   * FAS_ERR_UNSUPPORTED; fas_attention_backward rejects dropout_p > 0. */
+  float dropout_p;
+  int32_t reserved2;
+  uint64_t dropout_seed;
+  uint64_t dropout_offset;
 } fas_attn_args;
 
 int fas_abi_version(void);
@@ -181,7 +199,8 @@ int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64
                                                    void* stream);
 
 /* Replaces the forward half of flash.py:264-297 (attention ->
- * FlashAttention.forward :34-170, _fwd_kernel :335-500) without dropout:
+ * FlashAttention.forward :34-170, _fwd_kernel :335-500), with dropout as
+ * fas_attn_args describes (flash.py:459-466, 488-491):
  * out = softmax(mask(q k^T sm_scale)) v, and lse (B, Hq, M) fp32 with
  * element strides lse_stride receives the natural-log normalizer
  * m * sm_scale + ln(l), -inf for rows that see no key (flash.py:477-483).
@@ -200,7 +219,8 @@ int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t 
                         float* total, const int64_t total_stride[3], void* stream);
 
 /* Replaces FlashAttention.backward (flash.py:172-261, kernels :532-918)
- * without dropout.  a->out is the forward output O and lse its normalizer;
+ * without dropout (dropout_p > 0 returns FAS_ERR_UNSUPPORTED).  a->out is
+ * the forward output O and lse its normalizer;
  * dout is dL/dO (shaped like out).  Writes dq (like q) and dk, dv
  * (B, Hk, N, D) in the input dtype, dk and dv summed over the Hq/Hk query
  * heads of each KV head.  Needs fas_workspace_bytes(

@@ -46,7 +46,10 @@ from __future__ import annotations
 import math
 from typing import Iterable
 
+import numpy as np
 import torch
+
+from . import philox
 
 ALL_OUTPUTS = ("out", "scores", "row_sum", "col_sum", "col_softmax", "cross_qk", "cross_softmax")
 
@@ -90,7 +93,8 @@ def admissible_mask(i0: int, i1: int, N: int, causal: bool, causal_offset: int) 
 def reference_forward(q, k, v, *, causal: bool, sm_scale: float | None = None,
                       causal_offset: int | None = None, split: int | None = None,
                       want: Iterable[str] = ALL_OUTPUTS, chunk: int = 1024,
-                      heads: Iterable[int] | None = None) -> dict:
+                      heads: Iterable[int] | None = None, dropout=None,
+                      drop_scale: float = 1.0, drop_col_softmax: bool = False) -> dict:
     """Streams the oracle over (batch, query head, row chunk).
 
     q: (B, Hq, M, D); k, v: (B, Hk, N, D), any dtype/device (converted to
@@ -101,6 +105,10 @@ def reference_forward(q, k, v, *, causal: bool, sm_scale: float | None = None,
       out (B,Hq,M,D) fp32, scores (B,Hq,M,N) fp32 with -inf at masked pairs,
       row_sum (B,Hq,M), col_sum / col_softmax (B,Hk,N),
       cross_qk / cross_softmax (B,Hk,split).
+    dropout = (p, seed, offset) drops weight (b, h, i, j) from O (and from the
+    softmax column sum when drop_col_softmax) unless oracle.philox.keep_mask
+    keeps it; the row normaliser sums the weights before dropout, and O is
+    multiplied by drop_scale (attention_with_scores.py:165-203).
     """
     want = set(want)
     unknown = want - set(ALL_OUTPUTS)
@@ -149,14 +157,20 @@ def reference_forward(q, k, v, *, causal: bool, sm_scale: float | None = None,
                 if need_p:
                     p = torch.softmax(s, dim=-1)
                     p = torch.nan_to_num(p, nan=0.0)  # rows with no admissible key
+                pd = p if need_p else None
+                if need_p and dropout is not None:
+                    kept = philox.keep_mask(dropout[1], dropout[2], dropout[0], b, h,
+                                            range(i0, i1), N, Hq, M)
+                    pd = p * torch.from_numpy(kept)
                 if "out" in want:
-                    res["out"][b, h, i0:i1] = torch.matmul(p, vh)
+                    res["out"][b, h, i0:i1] = torch.matmul(pd, vh) * drop_scale
                 if "row_sum" in want:
                     res["row_sum"][b, h, i0:i1] = s0.sum(dim=-1)
                 if "col_sum" in want:
                     res["col_sum"][b, hk] += s0.sum(dim=0, dtype=torch.float64)
                 if "col_softmax" in want:
-                    res["col_softmax"][b, hk] += p.sum(dim=0, dtype=torch.float64)
+                    pc = pd if drop_col_softmax else p
+                    res["col_softmax"][b, hk] += pc.sum(dim=0, dtype=torch.float64)
                 r0 = max(i0, split) if split is not None else i1
                 if r0 < i1:
                     if "cross_qk" in want:
@@ -200,13 +214,30 @@ ENTRY_POINT_OUTPUT = {
 }
 
 
+# Entry points whose O is rescaled by 1/(1 - p) under dropout
+# (attention_with_scores.py:200-203; flash.py:488-491); the others are not.
+DROPOUT_RESCALES = {"attention_with_scores", "attention"}
+
+
+def dropout_scale(p: float) -> float:
+    """1.0 / (1.0 - p) as the reference's kernels compute it, in fp32."""
+    return float(np.float32(1.0) / (np.float32(1.0) - np.float32(p)))
+
+
 def oracle_for(entry_point: str, q, k, v, *, causal: bool, sm_scale=None, split=None,
-               chunk: int = 1024) -> tuple[torch.Tensor, torch.Tensor]:
-    """(out, side product) the named entry point must reproduce."""
+               chunk: int = 1024, dropout=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(out, side product) the named entry point must reproduce; dropout is
+    None or (p, seed, offset) as the launch drew it.  The buffered cross
+    softmax sum ignores dropout (attention_cross_token_softmax_sum.py:639-732)."""
     side = ENTRY_POINT_OUTPUT[entry_point]
+    if entry_point == "attention_cross_token_softmax_sum_buffered":
+        dropout = None
+    scale = dropout_scale(dropout[0]) if dropout and entry_point in DROPOUT_RESCALES else 1.0
     res = reference_forward(q, k, v, causal=causal, sm_scale=sm_scale,
                             causal_offset=ENTRY_POINT_OFFSET[entry_point], split=split,
-                            want=("out", side), chunk=chunk)
+                            want=("out", side), chunk=chunk, dropout=dropout,
+                            drop_scale=scale,
+                            drop_col_softmax=entry_point == "attention_with_softmax_col_sum")
     out, extra = res["out"], res[side]
     if side == "scores":
         extra = scores_as_returned(extra)

@@ -1,0 +1,138 @@
+"""Dropout with the reference's random stream, on the GPU.
+
+The reference keeps weight (b, h, i, j) iff Triton's tl.rand(seed, offset +
+((b*H + h)*M + i)*N + j, n_rounds=6) > p, with (seed, offset) drawn from the
+device generator by dropout.py:5-15.  The kernels' keep decisions are
+checked bit for bit against oracle/philox.py (itself pinned to Random123's
+known-answer vectors), and every entry point's outputs against the oracle
+with the reference's per-entry-point semantics: O everywhere, rescaled by
+1/(1-p) only in attention_with_scores and attention; the softmax column sum
+masked; other side products unaffected; the buffered cross softmax sum
+ignoring dropout.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import flash_attn_with_score_amd as fas
+from oracle import inputs, naive, philox
+from tests.tolerances import assert_out_close, assert_scores_close, assert_sum_close
+
+pytestmark = pytest.mark.gpu
+P = 0.3
+
+
+def _gen(gpu):
+    torch.cuda.init()  # the generators exist once the device is initialised
+    return torch.cuda.default_generators[gpu.index or 0]
+
+
+def _state(gpu):
+    w = _gen(gpu).get_state().view(torch.int64)
+    return int(w[0]), int(w[1])
+
+
+def _set_state(gpu, seed, offset):
+    g = _gen(gpu)
+    st = g.get_state()
+    w = st.view(torch.int64)
+    w[0], w[1] = seed, offset
+    g.set_state(st)
+
+
+def _ceil4(x):
+    return (x + 3) // 4 * 4
+
+
+@pytest.mark.parametrize("offset", [0, 123456, 2**31 + 1000], ids=["zero", "small", "wide"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("ep", ["attention_with_scores", "attention_with_row_sum"])
+def test_keep_mask_bit_exact(ep, offset, causal, gpu):
+    """With V = I (N = D) the output row i is keep_i * P_i / l_i (* scale):
+    its zeros are exactly the dropped or inadmissible pairs."""
+    B, H, M, N, D = 1, 3, 96, 64, 64
+    seed = 0x0123456789ABCDEF
+    print(f"[case] keep mask {ep} offset={offset} causal={causal}", flush=True)
+    q, k, _ = inputs.make_qkv(B, H, H, M, N, D, dtype=torch.float16, seed=3, scale=0.5)
+    v = torch.eye(N, D, dtype=torch.float16).expand(B, H, N, D).contiguous()
+    _set_state(gpu, seed, offset)
+    out, _ = getattr(fas, ep)(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal, dropout_p=P)
+    torch.cuda.synchronize()
+    assert _state(gpu) == (seed, offset + _ceil4(B * H * M * N))
+    got = (out.cpu() != 0).numpy()
+    adm = naive.admissible_mask(0, M, N, causal, N - M).numpy()
+    for h in range(H):
+        keep = philox.keep_mask(seed, offset, P, 0, h, range(M), N, H, M)
+        assert np.array_equal(got[0, h], keep & adm), f"head {h}"
+
+
+EPS = ["attention_with_scores", "attention_with_row_sum", "attention_with_col_sum",
+       "attention_with_col_sum_sequential", "attention_with_softmax_col_sum",
+       "attention_cross_token_qk_sum", "attention_cross_token_softmax_sum"]
+SHAPES = [(1, 4, 2, 200, 200, 64), (2, 3, 1, 130, 300, 128), (1, 4, 2, 32, 2048, 128)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}K{}M{}N{}D{}".format(*s))
+@pytest.mark.parametrize("ep", EPS)
+def test_entry_points_with_dropout(ep, shape, causal, dtype, gpu):
+    B, Hq, Hk, M, N, D = shape
+    split = N // 2 if "cross" in ep else None
+    seed, offset = 2024 + len(ep), 4096 * (1 + B)
+    print(f"[case] dropout {ep} {shape} causal={causal} {dtype}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=11)
+    _set_state(gpu, seed, offset)
+    fn = getattr(fas, ep)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    if split is None:
+        out, extra = fn(qd, kd, vd, causal=causal, dropout_p=P)
+    else:
+        out, extra = fn(qd, kd, vd, split, causal=causal, dropout_p=P)
+    torch.cuda.synchronize()
+    assert _state(gpu) == (seed, offset + _ceil4(B * Hq * M * N))
+    ref_out, ref_extra = naive.oracle_for(ep, q, k, v, causal=causal, split=split,
+                                          dropout=(P, seed, offset))
+    assert_out_close(out, ref_out)
+    if naive.ENTRY_POINT_OUTPUT[ep] == "scores":
+        assert_scores_close(extra, ref_extra)
+    else:
+        assert_sum_close(extra, ref_extra, naive.ENTRY_POINT_OUTPUT[ep])
+
+
+def test_buffered_ignores_dropout(gpu):
+    """attention_cross_token_softmax_sum_buffered ignores dropout_p and draws
+    no seed (attention_cross_token_softmax_sum.py:639-732)."""
+    q, k, v = inputs.make_qkv(1, 4, 2, 300, 300, 64, dtype=torch.float16, seed=5, device=gpu)
+    _set_state(gpu, 9, 100)
+    o1, x1 = fas.attention_cross_token_softmax_sum_buffered(q, k, v, 150, causal=True,
+                                                            dropout_p=P)
+    assert _state(gpu) == (9, 100)
+    o0, x0 = fas.attention_cross_token_softmax_sum_buffered(q, k, v, 150, causal=True)
+    assert torch.equal(o0, o1) and torch.equal(x0, x1)
+
+
+def test_attention_dropout(gpu):
+    """attention(): O with dropout and the 1/(1-p) rescale, L as without
+    dropout, (seed, offset) returned; the backward is not implemented."""
+    B, H, M, N, D = 1, 4, 200, 264, 64
+    q, k, v = inputs.make_qkv(B, H, 2, M, N, D, dtype=torch.float16, seed=8)
+    seed, offset = 31337, 640
+    _set_state(gpu, seed, offset)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    o, L, tot, s, off = fas.attention(qd, kd, vd, causal=True, dropout_p=P,
+                                      return_log_normalizer=True, return_seed_offset=True)
+    torch.cuda.synchronize()
+    assert (s, off) == (seed, offset)
+    ref = naive.reference_forward(q, k, v, causal=True, want=("out",), dropout=(P, seed, offset),
+                                  drop_scale=naive.dropout_scale(P))
+    assert_out_close(o, ref["out"])
+    _, L0, _, s0, off0 = fas.attention(qd, kd, vd, causal=True, return_log_normalizer=True,
+                                       return_seed_offset=True)
+    assert s0 is None and off0 is None
+    assert torch.equal(L, L0)
+    og = fas.attention(qd.requires_grad_(True), kd, vd, causal=True, dropout_p=P)
+    with pytest.raises(NotImplementedError, match="dropout"):
+        og.sum().backward()

@@ -40,7 +40,7 @@ def header_functions():
 
 
 def test_library_loads_with_abi_version(lib):
-    assert lib.fas_abi_version() == _native.ABI_VERSION == 4
+    assert lib.fas_abi_version() == _native.ABI_VERSION == 5
 
 
 def test_exports_match_header(lib):
@@ -272,13 +272,13 @@ def test_launcher_keeps_reference_asserts(fn):
 
 @pytest.mark.parametrize("fn", sorted(fas.__all__))
 def test_launcher_fails_loudly_without_device(fn):
-    """No CPU fallback: host tensors are rejected, dropout > 0 is refused."""
+    """No CPU fallback: host tensors are rejected, with or without dropout."""
     f = getattr(fas, fn)
     args = (16,) if "cross" in fn else ()
     q, k, v = _cpu_qkv()
     with pytest.raises(RuntimeError, match="HIP device"):
         f(q, k, v, *args, causal=True)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="HIP device"):
         f(q, k, v, *args, causal=True, dropout_p=0.1)
     with pytest.raises(AssertionError):
         f(q.float(), k.float(), v.float(), *args)
@@ -297,3 +297,36 @@ def test_rows_aligned_helper():
     x = torch.zeros(2, 3, 5, 64, dtype=torch.float16)
     assert _common._rows_aligned(x)
     assert not _common._rows_aligned(x[..., 1:])
+
+
+def test_dropout_requests(lib):
+    """Dropout arguments are validated before anything is launched."""
+    st3 = _native._I64x3(1, 1, 1)
+    st4 = _native._I64x4(1, 1, 1, 1)
+    for bad in (1.0, -0.25, float("nan")):
+        a = make_args()
+        a.dropout_p = bad
+        rc = lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st3, None, 0, None)
+        assert rc == _native.FAS_ERR_INVALID and "dropout_p" in _err(lib)
+    # a 64-bit offset with an element index past 2^31: the reference's index
+    # would depend on its block sizes
+    a = make_args(B=1, Hq=4, Hk=4, M=32768, N=32768, D=64)
+    a.dropout_p, a.dropout_offset = 0.1, 2**31
+    rc = lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st3, None, 0, None)
+    assert rc == _native.FAS_ERR_UNSUPPORTED and "2^31" in _err(lib)
+    # the backward pass has no dropout
+    a = make_args()
+    a.dropout_p = 0.1
+    rc = lib.fas_attention_backward(ctypes.byref(a), 0x10000, st4, 0x10000, st3, 0x10000, st4,
+                                    0x10000, st4, 0x10000, st4, None, 0, None)
+    assert rc == _native.FAS_ERR_UNSUPPORTED and "dropout" in _err(lib)
+
+
+def test_dropout_p_checked_in_python():
+    import torch
+    from flash_attn_with_score_amd import _common
+
+    t = torch.zeros(1, 1, 4, 16, dtype=torch.float16)
+    for bad in (1.0, -0.1):
+        with pytest.raises(ValueError, match="dropout_p"):
+            _common.check_device_inputs(t, t, t, bad)
