@@ -180,7 +180,7 @@ def measured_traffic(key):
     return None, None
 
 
-def make_call(fas, name, q, k, v, causal, split):
+def make_call(fas, name, q, k, v, causal, split, dropout_p=0.0):
     if name == "attention_bwd":
         # One forward outside the timed calls; each call is one backward pass
         # through the autograd graph (dq, dk, dv).
@@ -194,8 +194,8 @@ def make_call(fas, name, q, k, v, causal, split):
         return lambda: compute_attention_scores(q, k)
     fn = getattr(fas, WORKLOADS[name][0])
     if WORKLOADS[name][1]:
-        return lambda: fn(q, k, v, split, causal=causal)
-    return lambda: fn(q, k, v, causal=causal)
+        return lambda: fn(q, k, v, split, causal=causal, dropout_p=dropout_p)
+    return lambda: fn(q, k, v, causal=causal, dropout_p=dropout_p)
 
 
 def time_steps(call, steps: int, warmup: int):
@@ -235,6 +235,8 @@ def main() -> int:
     ap.add_argument("--split", type=int, default=None)
     ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
     ap.add_argument("--non-causal", action="store_true")
+    ap.add_argument("--dropout", type=float, default=0.0,
+                    help="dropout_p of the forward workloads (default 0, as every config)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU-oracle work for cpu_baseline (0 disables)")
     ap.add_argument("--no-secondary", action="store_true")
@@ -273,7 +275,10 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0, device=dev)
-    call = make_call(fas, args.workload, q, k, v, causal, split)
+    if args.dropout and args.workload in ("attention_bwd", "scores_only"):
+        print(f"--dropout does not apply to {args.workload}", file=sys.stderr)
+        return 2
+    call = make_call(fas, args.workload, q, k, v, causal, split, args.dropout)
     wall, dev_ms = time_steps(call, args.steps, args.warmup)
     flop, nbytes = work(args.workload, B, H, Hk, M, N, D, causal, split)
     ms = wall * 1e3 / args.steps
@@ -314,7 +319,8 @@ def main() -> int:
                                + (f" split{split}" if split else ""),
                    "batch": B, "heads_q": H, "heads_k": Hk, "seqlen": M, "seqlen_k": N,
                    "head_dim": D,
-                   "causal": causal, "split": split, "parallelism": "none (1 GPU)"},
+                   "causal": causal, "split": split, "dropout_p": args.dropout,
+                   "parallelism": "none (1 GPU)"},
         "flop_convention": "4*B*H*D*(admissible pairs) (causal work); "
                            "reference convention 4*B*H*M*N*D in tflops_ref_convention",
         "tflops_ref_convention": round(4 * B * H * M * N * D / (ms * 1e-3) / 1e12, 2),
