@@ -185,7 +185,7 @@ def make_call(fas, name, q, k, v, causal, split, dropout_p=0.0):
         # One forward outside the timed calls; each call is one backward pass
         # through the autograd graph (dq, dk, dv).
         qg, kg, vg = (t.detach().requires_grad_(True) for t in (q, k, v))
-        o = fas.attention(qg, kg, vg, causal=causal)
+        o = fas.attention(qg, kg, vg, causal=causal, dropout_p=dropout_p)
         g = torch.Generator(device=q.device).manual_seed(1)
         do = torch.randn(o.shape, generator=g, device=q.device, dtype=o.dtype)
         return lambda: torch.autograd.grad(o, (qg, kg, vg), do, retain_graph=True)
@@ -275,7 +275,7 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
     q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0, device=dev)
-    if args.dropout and args.workload in ("attention_bwd", "scores_only"):
+    if args.dropout and args.workload == "scores_only":
         print(f"--dropout does not apply to {args.workload}", file=sys.stderr)
         return 2
     call = make_call(fas, args.workload, q, k, v, causal, split, args.dropout)

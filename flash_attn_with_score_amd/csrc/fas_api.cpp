@@ -730,8 +730,6 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   Problem pr;
   int rc;
   if ((rc = check_args(fn, a, &pr))) return rc;
-  if (a->dropout_p > 0.f)
-    return fail(FAS_ERR_UNSUPPORTED, fn, "the backward pass with dropout_p > 0 is not implemented");
   if ((int64_t)pr.B * pr.H == 0) return FAS_OK;
   if (pr.M > 0) {
     if (gst == nullptr || qst == nullptr || lst == nullptr || lse == nullptr)
@@ -790,6 +788,9 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   p.sm_scale = std::fabs(pr.sm_scale);
   p.scale_signed = pr.sm_scale;
   p.qk_scale = qk_scale_of(pr.sm_scale);
+  p.dropout = a->dropout_p > 0.f ? 1 : 0;
+  p.drop = drop_params(a, pr);
+  if (p.dropout) p.drop.scale = 1.f / (1.f - a->dropout_p);
   return hip_status(fn, fas::launch_bwd(p, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
 }
 

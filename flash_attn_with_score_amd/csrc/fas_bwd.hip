@@ -4,16 +4,16 @@
 
 namespace fas {
 
-template <class E, int D>
-static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
+template <class E, int D, bool DROP>
+static hipError_t bwd_drop_t(const BwdParams& p, hipStream_t s) {
   const int64_t bh = (int64_t)p.B * p.H;
   if (p.M > 0)
     hipLaunchKernelGGL((bwd_prep_kernel<E, D>), dim3((unsigned)(bh * p.nprep)), dim3(256), 0, s,
                        p);
   if (p.N > 0) {
     const int64_t rest = p.partial ? bh : (int64_t)p.B * p.Hk;
-    hipLaunchKernelGGL((bwd_dkdv_kernel<E, D>), dim3((unsigned)(rest * p.nkb)), dim3(256), 0, s,
-                       p);
+    hipLaunchKernelGGL((bwd_dkdv_kernel<E, D, DROP>), dim3((unsigned)(rest * p.nkb)), dim3(256),
+                       0, s, p);
     if (p.partial) {
       const int64_t total = (int64_t)p.B * p.Hk * p.N * (D / 8);
       int64_t blocks = (total + 255) / 256;
@@ -23,8 +23,14 @@ static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
     }
   }
   if (p.M > 0)
-    hipLaunchKernelGGL((bwd_dq_kernel<E, D>), dim3((unsigned)(bh * p.nrb)), dim3(256), 0, s, p);
+    hipLaunchKernelGGL((bwd_dq_kernel<E, D, DROP>), dim3((unsigned)(bh * p.nrb)), dim3(256), 0, s,
+                       p);
   return hipGetLastError();
+}
+
+template <class E, int D>
+static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
+  return p.dropout ? bwd_drop_t<E, D, true>(p, s) : bwd_drop_t<E, D, false>(p, s);
 }
 
 hipError_t launch_bwd(const BwdParams& p, int dtype, int d, hipStream_t s) {

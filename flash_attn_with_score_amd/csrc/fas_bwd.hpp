@@ -95,7 +95,10 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdParams p) {
 
 // ---------------------------------------------------------------- dK, dV
 
-template <class E, int D>
+// DROP: the forward's dropout mask Z (keep = 1) and r = 1/(1-p) enter as
+// dV = r sum_i (Z P)_ij dO_i and dS = P (r Z dP - delta) (flash.py:705-731);
+// the dP accumulator then starts at 0 and delta is added afterwards.
+template <class E, int D, bool DROP>
 __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
   constexpr int KS = D / 16;               // k-steps over the head dim
   constexpr int DB = D >= 32 ? D / 32 : 1;  // 32-dim blocks of dK^T / dV^T
@@ -195,8 +198,12 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
         const int r0 = t * TQ + 32 * qb;
         // Register r holds query row r0 + acc_row(r, g) and key key0 + c.
         f32x16 s = f32x16{}, dp;
-        load8(dp, &xlds[stage][32 * qb + 8 * g], 0, 0);
-        load8(dp, &xlds[stage][32 * qb + 16 + 8 * g], 0, 1);
+        if constexpr (DROP) {
+          dp = f32x16{};
+        } else {
+          load8(dp, &xlds[stage][32 * qb + 8 * g], 0, 0);
+          load8(dp, &xlds[stage][32 * qb + 16 + 8 * g], 0, 1);
+        }
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
           s = E::mma(lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g), kreg[ks], s);
@@ -212,8 +219,18 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
           if constexpr (MASK) {
             if (p.causal_off + r0 + acc_row(r, g) < key0 + c) pr = 0.f;
           }
-          s[r] = pr;
-          dp[r] = pr * dp[r];
+          if constexpr (DROP) {
+            const uint32_t idx =
+                ((uint32_t)bh * (uint32_t)p.M + (uint32_t)(r0 + acc_row(r, g))) *
+                    (uint32_t)p.N + (uint32_t)(key0 + c);
+            const bool keep = dropout_keep(p.drop, idx);
+            const float nd = xlds[stage][32 * qb + acc_row(r, g)];  // -delta
+            s[r] = keep ? pr : 0.f;
+            dp[r] = pr * ((keep ? p.drop.scale * dp[r] : 0.f) + nd);
+          } else {
+            s[r] = pr;
+            dp[r] = pr * dp[r];
+          }
         }
         const u32x4 pb0 = pack_b<E>(s, 0), pb1 = pack_b<E>(s, 1);
         const u32x4 sb0 = pack_b<E>(dp, 0), sb1 = pack_b<E>(dp, 1);
@@ -257,6 +274,10 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
   const int key = key0 + c;
   if (key >= p.N) return;
   const float ks_ = p.scale_signed;
+  if constexpr (DROP) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db) dv[db] *= p.drop.scale;
+  }
   if (!p.partial) {
     uint16_t* dkr = p.dk + b * p.sdk0 + hk * p.sdk1 + (int64_t)key * p.sdk2;
     uint16_t* dvr = p.dv + b * p.sdv0 + hk * p.sdv1 + (int64_t)key * p.sdv2;
@@ -326,7 +347,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(const BwdParams p)
 
 // ---------------------------------------------------------------- dQ
 
-template <class E, int D>
+// DROP: dS = P (r Z dP - delta) as in the dK/dV kernel (flash.py:885-895).
+template <class E, int D, bool DROP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_kernel(const BwdParams p) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
@@ -361,6 +383,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // Rows past M read nl = -inf (padding), so their P is 0.
   const float nl = p.nl[(int64_t)bh * p.Mpad + qrow];
   const float xl = p.delta[(int64_t)bh * p.Mpad + qrow];
+  const uint32_t drow = ((uint32_t)bh * (uint32_t)p.M + (uint32_t)qrow) * (uint32_t)p.N;
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(qreg[ks]), "+v"(greg[ks]));
 
@@ -417,7 +440,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       // Register r holds key kbase + acc_row(r, g) for query row qrow.
       f32x16 s = f32x16{}, dp;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) dp[r] = xl;
+      for (int r = 0; r < 16; ++r) dp[r] = DROP ? 0.f : xl;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         s = E::mma(ak[ks], qreg[ks], s);
@@ -439,7 +462,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           const int key = kbase + acc_row(r, g);
           if (key >= p.N || (p.causal && p.causal_off + qrow < key)) pr = 0.f;
         }
-        dp[r] = pr * dp[r];
+        if constexpr (DROP) {
+          const uint32_t idx = drow + (uint32_t)(kbase + acc_row(r, g));
+          dp[r] = pr * ((dropout_keep(p.drop, idx) ? p.drop.scale * dp[r] : 0.f) + xl);
+        } else {
+          dp[r] = pr * dp[r];
+        }
       }
       const u32x4 sb0 = pack_b<E>(dp, 0), sb1 = pack_b<E>(dp, 1);
       __builtin_amdgcn_sched_barrier(0);

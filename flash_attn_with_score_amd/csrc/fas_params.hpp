@@ -149,6 +149,8 @@ struct BwdParams {
   float sm_scale;        // |sm_scale|
   float scale_signed;    // sm_scale with its sign: dQ = s sum_j dS_ij k_j, dK = s sum_i dS_ij q_i
   float qk_scale;        // |sm_scale| * log2(e)
+  int dropout;           // 1: the dropout instances (flash.py:653-659, 705-731, 843-890)
+  DropParams drop;       // scale = 1/(1-p)
 };
 
 }  // namespace fas

@@ -49,9 +49,8 @@ def _forward(q, k, v, causal, sm_scale, want_total, dropout_p):
 
 
 class FlashAttention(torch.autograd.Function):
-    """flash.py:32-261.  The forward applies dropout (flash.py:59-66, 459-466,
-    488-491); the backward of a forward with dropout_p > 0 raises
-    NotImplementedError."""
+    """flash.py:32-261, with dropout in the forward (flash.py:59-66, 459-466,
+    488-491) and the backward (:653-659, 705-731, 843-895)."""
 
     @staticmethod
     def forward(ctx, q, k, v, causal, sm_scale, dropout_p, return_log_normalizer,
@@ -63,7 +62,7 @@ class FlashAttention(torch.autograd.Function):
         ctx.save_for_backward(p.q, p.k, p.v, o, L)
         ctx.sm_scale = p.sm_scale
         ctx.causal = causal
-        ctx.dropout_p = dropout_p
+        ctx.drop = drop
         if return_log_normalizer or return_total_attention or return_seed_offset:
             # seed and offset only with dropout and return_seed_offset
             # (flash.py:161-169).
@@ -75,9 +74,6 @@ class FlashAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, do, *ignored):
-        if ctx.dropout_p > 0.0:
-            raise NotImplementedError(
-                "flash_attn_with_score_amd: attention() backward with dropout_p > 0")
         q, k, v, o, L = ctx.saved_tensors
         B, H, M, D = q.shape
         Hk, N = k.shape[1], k.shape[2]
@@ -85,7 +81,8 @@ class FlashAttention(torch.autograd.Function):
         dq = _common.new_output(q)
         dk = torch.empty((B, Hk, N, D), dtype=k.dtype, device=q.device)
         dv = torch.empty((B, Hk, N, D), dtype=v.dtype, device=q.device)
-        args = _native.make_args(q, k, v, o, ctx.causal, ctx.sm_scale)
+        # The forward's (p, seed, offset): the same keep mask (flash.py:653-659).
+        args = _native.make_args(q, k, v, o, ctx.causal, ctx.sm_scale, ctx.drop)
         ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args, 0,
                                                  q.device)
         _common.call("fas_attention_backward", q, ctypes.byref(args), do.data_ptr(),

@@ -107,7 +107,8 @@ typedef struct fas_attn_args {
    * fas_attention_with_softmax_col_sum, nothing else.  The buffered cross
    * softmax sum, the scores-only call, the total attention and the score and
    * raw-sum outputs ignore it.  Offsets >= 2^31 with B*Hq*M*N >= 2^31 return
-   * FAS_ERR_UNSUPPORTED; fas_attention_backward rejects dropout_p > 0. */
+   * FAS_ERR_UNSUPPORTED.  fas_attention_backward takes the forward's dropout
+   * fields and regenerates the same mask. */
   float dropout_p;
   int32_t reserved2;
   uint64_t dropout_seed;
@@ -219,8 +220,8 @@ int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t 
                         float* total, const int64_t total_stride[3], void* stream);
 
 /* Replaces FlashAttention.backward (flash.py:172-261, kernels :532-918)
- * without dropout (dropout_p > 0 returns FAS_ERR_UNSUPPORTED).  a->out is
- * the forward output O and lse its normalizer;
+ * with the forward's dropout (flash.py:653-731, 843-895).  a->out is the
+ * forward output O and lse its normalizer;
  * dout is dL/dO (shaped like out).  Writes dq (like q) and dk, dv
  * (B, Hk, N, D) in the input dtype, dk and dv summed over the Hq/Hk query
  * heads of each KV head.  Needs fas_workspace_bytes(

@@ -245,13 +245,15 @@ def oracle_for(entry_point: str, q, k, v, *, causal: bool, sm_scale=None, split=
 
 
 def attention_reference(q, k, v, do=None, *, causal: bool, sm_scale: float | None = None,
-                        causal_offset: int | None = None) -> dict:
+                        causal_offset: int | None = None, dropout=None) -> dict:
     """fp64 CPU restatement of attention() and its backward pass.
 
     Returns out (B,Hq,M,D), lse (B,Hq,M) and total (B,Hq,N) and, when do
     (shaped like out) is given, dq (like q), dk and dv (like k): the
     gradients of sum(out * do).  causal_offset defaults to N - M
-    (bottom-right, flash.py:447).
+    (bottom-right, flash.py:447).  dropout = (p, seed, offset): out uses the
+    weights times the keep mask of oracle.philox.keep_mask and 1/(1-p)
+    (flash.py:459-466, 488-491); lse and total are the undropped ones.
     """
     q, k, v = (t.detach().to("cpu", torch.float64) for t in (q, k, v))
     B, Hq, M, D = q.shape
@@ -289,7 +291,13 @@ def attention_reference(q, k, v, do=None, *, causal: bool, sm_scale: float | Non
             s = s.masked_fill(~use, float("-inf"))
             lse = torch.logsumexp(s, dim=-1, keepdim=True)
             p = torch.exp(s - lse) * row_has
-            o = torch.matmul(p, vv)
+            pd = p
+            if dropout is not None:
+                z = np.stack([philox.keep_mask(dropout[1], dropout[2], dropout[0], b, h,
+                                               range(M), N, Hq, M)
+                              for h in range(hk * G, (hk + 1) * G)])
+                pd = p * torch.from_numpy(z).to(torch.float64) * dropout_scale(dropout[0])
+            o = torch.matmul(pd, vv)
             res["out"][b, hs] = o.detach()
             res["lse"][b, hs] = torch.where(has_key, lse.detach().squeeze(-1),
                                             torch.full((), float("-inf"), dtype=torch.float64))

@@ -114,11 +114,16 @@ def test_buffered_ignores_dropout(gpu):
     assert torch.equal(o0, o1) and torch.equal(x0, x1)
 
 
-def test_attention_dropout(gpu):
+@pytest.mark.parametrize("shape", [(1, 4, 2, 200, 264, 64), (2, 2, 2, 300, 160, 128),
+                                   (1, 6, 2, 96, 520, 32)],
+                         ids=lambda s: "B{}H{}K{}M{}N{}D{}".format(*s))
+def test_attention_dropout(shape, gpu):
     """attention(): O with dropout and the 1/(1-p) rescale, L as without
-    dropout, (seed, offset) returned; the backward is not implemented."""
-    B, H, M, N, D = 1, 4, 200, 264, 64
-    q, k, v = inputs.make_qkv(B, H, 2, M, N, D, dtype=torch.float16, seed=8)
+    dropout, (seed, offset) returned, and dq, dk, dv through the same mask
+    (flash.py:653-731, 843-895) against the fp64 oracle."""
+    B, H, Hk, M, N, D = shape
+    print(f"[case] attention dropout {shape}", flush=True)
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=torch.float16, seed=8)
     seed, offset = 31337, 640
     _set_state(gpu, seed, offset)
     qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
@@ -133,6 +138,14 @@ def test_attention_dropout(gpu):
                                        return_seed_offset=True)
     assert s0 is None and off0 is None
     assert torch.equal(L, L0)
-    og = fas.attention(qd.requires_grad_(True), kd, vd, causal=True, dropout_p=P)
-    with pytest.raises(NotImplementedError, match="dropout"):
-        og.sum().backward()
+    g = torch.Generator("cpu").manual_seed(21)
+    do = torch.randn(q.shape, generator=g).to(torch.float16)
+    qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (qd, kd, vd))
+    _set_state(gpu, seed, offset)
+    og = fas.attention(qg, kg, vg, causal=True, dropout_p=P)
+    dq, dk, dv = torch.autograd.grad(og, (qg, kg, vg), do.to(gpu))
+    torch.cuda.synchronize()
+    r = naive.attention_reference(q, k, v, do, causal=True, dropout=(P, seed, offset))
+    assert_out_close(og, r["out"])
+    for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+        assert_out_close(got, r[name])

@@ -314,12 +314,12 @@ def test_dropout_requests(lib):
     a.dropout_p, a.dropout_offset = 0.1, 2**31
     rc = lib.fas_attention_with_row_sum(ctypes.byref(a), 0x10000, st3, None, 0, None)
     assert rc == _native.FAS_ERR_UNSUPPORTED and "2^31" in _err(lib)
-    # the backward pass has no dropout
+    # the backward pass validates dropout_p like the forward
     a = make_args()
-    a.dropout_p = 0.1
+    a.dropout_p = 1.5
     rc = lib.fas_attention_backward(ctypes.byref(a), 0x10000, st4, 0x10000, st3, 0x10000, st4,
                                     0x10000, st4, 0x10000, st4, None, 0, None)
-    assert rc == _native.FAS_ERR_UNSUPPORTED and "dropout" in _err(lib)
+    assert rc == _native.FAS_ERR_INVALID and "dropout_p" in _err(lib)
 
 
 def test_dropout_p_checked_in_python():

@@ -320,3 +320,43 @@ def test_planted_gradient_without_group_sum_is_caught():
     r = naive.attention_reference(q[:, ::G], k, v, do[:, ::G], causal=causal, sm_scale=0.7)
     _, gk, _ = _fd_grads(q, k, v, do, causal, 0.7)
     assert not np.allclose(r["dk"].numpy(), gk, atol=1e-6)
+
+
+def test_attention_reference_dropout():
+    """Dropout in the fp64 attention oracle: with every weight kept the output
+    is 1/(1-p) times the undropped one; with some dropped, the autograd
+    gradients match central differences of its own forward (the mask is
+    fixed by (seed, offset), so the function is smooth)."""
+    from oracle import philox
+
+    case = (1, 2, 1, 5, 7, 4, True)
+    q, k, v, do, causal = _attn_inputs(case)
+    base = naive.attention_reference(q, k, v, causal=causal, sm_scale=0.7)
+    tiny = (1e-9, 5, 0)
+    assert all(philox.keep_mask(5, 0, 1e-9, 0, h, range(5), 7, 2, 5).all() for h in range(2))
+    kept = naive.attention_reference(q, k, v, causal=causal, sm_scale=0.7, dropout=tiny)
+    np.testing.assert_allclose(kept["out"].numpy(), base["out"].numpy() * naive.dropout_scale(1e-9),
+                               rtol=1e-12)
+    drop = (0.4, 12345, 64)
+    r = naive.attention_reference(q, k, v, do, causal=causal, sm_scale=0.7, dropout=drop)
+    assert not np.allclose(r["out"].numpy(), base["out"].numpy())
+    np.testing.assert_array_equal(r["lse"].numpy(), base["lse"].numpy())
+
+    def f(qq, kk, vv):
+        o = naive.attention_reference(torch.from_numpy(qq), torch.from_numpy(kk),
+                                      torch.from_numpy(vv), causal=causal, sm_scale=0.7,
+                                      dropout=drop)["out"]
+        return float((o.numpy() * do.numpy()).sum())
+
+    arrs = [t.numpy().copy() for t in (q, k, v)]
+    for which, name in enumerate(("dq", "dk", "dv")):
+        g = np.zeros_like(arrs[which])
+        for idx in np.ndindex(g.shape):
+            old = arrs[which][idx]
+            arrs[which][idx] = old + 1e-6
+            fp = f(*arrs)
+            arrs[which][idx] = old - 1e-6
+            fm = f(*arrs)
+            arrs[which][idx] = old
+            g[idx] = (fp - fm) / 2e-6
+        np.testing.assert_allclose(r[name].numpy(), g, atol=1e-6)
