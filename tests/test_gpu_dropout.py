@@ -114,16 +114,17 @@ def test_buffered_ignores_dropout(gpu):
     assert torch.equal(o0, o1) and torch.equal(x0, x1)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("shape", [(1, 4, 2, 200, 264, 64), (2, 2, 2, 300, 160, 128),
-                                   (1, 6, 2, 96, 520, 32)],
+                                   (1, 6, 2, 96, 520, 32), (1, 2, 1, 64, 300, 16)],
                          ids=lambda s: "B{}H{}K{}M{}N{}D{}".format(*s))
-def test_attention_dropout(shape, gpu):
+def test_attention_dropout(shape, dtype, gpu):
     """attention(): O with dropout and the 1/(1-p) rescale, L as without
     dropout, (seed, offset) returned, and dq, dk, dv through the same mask
     (flash.py:653-731, 843-895) against the fp64 oracle."""
     B, H, Hk, M, N, D = shape
-    print(f"[case] attention dropout {shape}", flush=True)
-    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=torch.float16, seed=8)
+    print(f"[case] attention dropout {shape} {dtype}", flush=True)
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=8)
     seed, offset = 31337, 640
     _set_state(gpu, seed, offset)
     qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
@@ -139,7 +140,7 @@ def test_attention_dropout(shape, gpu):
     assert s0 is None and off0 is None
     assert torch.equal(L, L0)
     g = torch.Generator("cpu").manual_seed(21)
-    do = torch.randn(q.shape, generator=g).to(torch.float16)
+    do = torch.randn(q.shape, generator=g).to(dtype)
     qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (qd, kd, vd))
     _set_state(gpu, seed, offset)
     og = fas.attention(qg, kg, vg, causal=True, dropout_p=P)
