@@ -13,11 +13,16 @@ resident in HBM.  The line printed is the driver's JSON contract plus
   secondary     the softmax column-sum kernel at the same shape against the
                 fp16 MFMA peak.
 
-The default warmup (300 steps, about 70 ms) is sized for the GPU's clock
-ramp: from idle, the first ~25 ms of calls run up to 30% slower while the
-clocks rise (measured on the MI355X: 302 us per scores call in the first
-5 ms, 231 us from ~25 ms on, at the 1400 W board power limit).  Timing fewer
-warmup steps measures the ramp, not the kernel.
+Before the counted warmup steps, every run pre-warms by time: it calls the
+step until at least --prewarm-ms (default 150 ms) of wall time has passed,
+whatever --warmup says.  From idle, the GPU needs ~25 ms of load to raise its
+clocks, and the first calls run up to 30% slower (measured on the MI355X: 302
+us per scores call in the first 5 ms, 231 us from ~25 ms on, at the 1400 W
+board power limit); a count of warmup calls alone (the driver passes
+--warmup 5) would time that ramp, not the kernel.  The reference's harness
+warms by time as well (triton.testing.do_bench(warmup=50), benchmark.py:254,
+352).  The line reports the pre-warm as "prewarm" and keeps "warmup" as
+passed.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -198,10 +203,28 @@ def make_call(fas, name, q, k, v, causal, split, dropout_p=0.0):
     return lambda: fn(q, k, v, causal=causal, dropout_p=dropout_p)
 
 
-def time_steps(call, steps: int, warmup: int):
+def prewarm(call, min_ms: float) -> dict:
+    """Calls `call` in batches of 10 until min_ms of wall time has passed
+    (synchronising after each batch), so the clocks have left their ramp
+    before anything is timed."""
+    calls = 0
+    t0 = time.perf_counter()
+    while min_ms > 0:
+        for _ in range(10):
+            call()
+        calls += 10
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= min_ms:
+            break
+    return {"ms": round((time.perf_counter() - t0) * 1e3, 1), "calls": calls}
+
+
+def time_steps(call, steps: int, warmup: int, prewarm_ms: float):
     """Wall time of `steps` calls, bracketed by synchronize, plus the average
     device time per call from HIP events on torch's current stream (the
-    stream the entry points launch on)."""
+    stream the entry points launch on).  A time-based pre-warm and then
+    `warmup` untimed calls come first."""
+    warm = prewarm(call, prewarm_ms)
     for _ in range(warmup):
         call()
     torch.cuda.synchronize()
@@ -216,7 +239,7 @@ def time_steps(call, steps: int, warmup: int):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     dev_ms = start.elapsed_time(end) / steps
-    return wall, dev_ms
+    return wall, dev_ms, warm
 
 
 def main() -> int:
@@ -224,6 +247,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--prewarm-ms", type=float, default=150.0,
+                    help="wall time of calls before the warmup steps (clock ramp; default 150)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="scores")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--heads", type=int, default=32)
@@ -279,7 +304,7 @@ def main() -> int:
         print(f"--dropout does not apply to {args.workload}", file=sys.stderr)
         return 2
     call = make_call(fas, args.workload, q, k, v, causal, split, args.dropout)
-    wall, dev_ms = time_steps(call, args.steps, args.warmup)
+    wall, dev_ms, warm = time_steps(call, args.steps, args.warmup, args.prewarm_ms)
     flop, nbytes = work(args.workload, B, H, Hk, M, N, D, causal, split)
     ms = wall * 1e3 / args.steps
     tflops = flop / (ms * 1e-3) / 1e12
@@ -307,6 +332,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm": warm,
         "ms_per_step": round(ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -332,7 +358,8 @@ def main() -> int:
 
     if not args.no_secondary and args.workload == "scores":
         call2 = make_call(fas, "col_softmax", q, k, v, causal, None)
-        _, dev2 = time_steps(call2, max(5, args.steps // 2), max(2, args.warmup // 2))
+        _, dev2, _ = time_steps(call2, max(5, args.steps // 2), max(2, args.warmup // 2),
+                                args.prewarm_ms)
         flop2, _ = work("col_softmax", B, H, Hk, M, N, D, causal, None)
         a2 = flop2 / (dev2 * 1e-3) / 1e12
         line["secondary"] = {"workload": f"attention_with_softmax_col_sum B{B} H{H} S{M} D{D} "

@@ -32,7 +32,9 @@ def attention_cross_token_qk_sum(
     heads of group hk of masked (q_i . k_j) * sm_scale, for j < split.
 
     out / cross_token_qk_out are optional caller buffers, validated as in
-    attention_cross_token_qk_sum.py:341-357; the latter is zeroed first.
+    attention_cross_token_qk_sum.py:341-357.  The kernels overwrite every
+    (B, Hk, split) element of cross_token_qk_out, so unlike the reference
+    (:363) it is not zeroed first and its prior contents do not matter.
     reuse_buffers is accepted and unused, as in the reference.
     """
     Dq, Dk, Dv = q.shape[-1], k.shape[-1], v.shape[-1]

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdint>
 #include <cstdlib>
 #include <string>
 
@@ -219,12 +220,18 @@ int zero_out3(const char* fn, float* out, const int64_t* st, int64_t n0, int64_t
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+struct SplitPlan {
+  int nsplit = 1, tps = 0;
+  int64_t mpad = 0;
+};
+
 struct Workspace {
   size_t lse = 0, part = 0, bsum = 0, region = 0, total = 0;  // byte offsets / total
   size_t nl = 0, delta = 0;                                     // backward row values
   size_t so = 0, sm = 0, sl = 0, sr = 0;                        // key-split partials
   bool has_lse = false, has_part = false, has_bsum = false, has_region = false;
   bool has_split = false;
+  SplitPlan sp;  // the forward's key split (nsplit 1: none)
 };
 
 // Key split of the plain / row-sum forward.  When the row blocks of the
@@ -235,12 +242,16 @@ struct Workspace {
 // query and the launch agree.  The scores variant splits only below 64 row
 // blocks: its split route writes the scores in a second kernel, which the
 // fused writer beats while it still has a quarter of the CUs busy.
-struct SplitPlan {
-  int nsplit = 1, tps = 0;
-  int64_t mpad = 0;
-};
 constexpr int64_t kScoresSplitMaxWgs = 64;
-SplitPlan split_plan(const Problem& pr, bool top_left, int64_t max_wgs = 255) {
+// Bytes of the fp32 partials of a plan (O, offset, weight sum, row sum).
+size_t split_bytes(const Problem& pr, const SplitPlan& sp) {
+  const size_t rows = (size_t)pr.B * pr.H * sp.nsplit * sp.mpad;
+  return align256(rows * pr.D * 4) + 3 * align256(rows * 4);
+}
+// max_bytes bounds the partials (the no-allocation entry point's scratch):
+// the plan then takes fewer, longer splits, or none.
+SplitPlan split_plan(const Problem& pr, bool top_left, int64_t max_wgs = 255,
+                     size_t max_bytes = SIZE_MAX) {
   SplitPlan sp;
   const int64_t nrb = ((int64_t)pr.M + fas::kFwdRows - 1) / fas::kFwdRows;
   const int64_t wgs = (int64_t)pr.B * pr.H * nrb;
@@ -249,14 +260,16 @@ SplitPlan split_plan(const Problem& pr, bool top_left, int64_t max_wgs = 255) {
   int64_t hi = pr.N;
   if (pr.causal) hi = std::min<int64_t>(pr.N, std::max<int64_t>(0, off + nrb * fas::kFwdRows));
   const int64_t nt = (hi + 63) / 64;
-  int64_t ns = std::min<int64_t>((512 + wgs - 1) / wgs, nt / 8);
-  if (ns < 2) return sp;
-  const int64_t tps = (nt + ns - 1) / ns;
-  ns = (nt + tps - 1) / tps;
-  if (ns < 2) return sp;
-  sp.nsplit = (int)ns;
-  sp.tps = (int)tps;
-  sp.mpad = nrb * fas::kFwdRows;
+  for (int64_t want = std::min<int64_t>((512 + wgs - 1) / wgs, nt / 8); want >= 2; --want) {
+    const int64_t tps = (nt + want - 1) / want;
+    const int64_t ns = (nt + tps - 1) / tps;
+    if (ns < 2) break;
+    SplitPlan c;
+    c.nsplit = (int)ns;
+    c.tps = (int)tps;
+    c.mpad = nrb * fas::kFwdRows;
+    if (split_bytes(pr, c) <= max_bytes) return c;
+  }
   return sp;
 }
 
@@ -291,7 +304,9 @@ int64_t ncols_of(int variant, const Problem& pr, int64_t split) {
   }
 }
 
-Workspace layout(int variant, const Problem& pr, int64_t split) {
+// budget: largest total the caller can provide (SIZE_MAX: any); only the
+// key-split partials adapt to it, by a smaller split.
+Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = SIZE_MAX) {
   Workspace w;
   size_t off = 0;
   const int64_t ncols = ncols_of(variant, pr, split);
@@ -328,12 +343,22 @@ Workspace layout(int variant, const Problem& pr, int64_t split) {
       off += align256((size_t)pr.B * pr.H * pr.N * 2 * pr.D * 4);
     }
   }
-  if (forward_can_split(variant)) {
+  if (raw) {
+    const int64_t row_lo = variant == FAS_VARIANT_CROSS_QK_SUM ? split : 0;
+    const int64_t rows = pr.M > row_lo ? pr.M - row_lo : 0;
+    const int64_t nblk = (rows + 63) / 64;
+    w.has_bsum = true;
+    w.bsum = off;
+    off += align256((size_t)pr.B * pr.Hk * (nblk + 1) * pr.D * 4);
+  }
+  if (forward_can_split(variant) && off <= budget) {
     const SplitPlan sp = split_plan(pr, variant == FAS_VARIANT_CROSS_QK_SUM,
-                                    variant == FAS_VARIANT_SCORES ? kScoresSplitMaxWgs : 255);
+                                    variant == FAS_VARIANT_SCORES ? kScoresSplitMaxWgs : 255,
+                                    budget - off);
     if (sp.nsplit > 1) {
       const size_t rows = (size_t)pr.B * pr.H * sp.nsplit * sp.mpad;
       w.has_split = true;
+      w.sp = sp;
       w.so = off;
       off += align256(rows * pr.D * 4);
       w.sm = off;
@@ -343,14 +368,6 @@ Workspace layout(int variant, const Problem& pr, int64_t split) {
       w.sr = off;
       off += align256(rows * 4);
     }
-  }
-  if (raw) {
-    const int64_t row_lo = variant == FAS_VARIANT_CROSS_QK_SUM ? split : 0;
-    const int64_t rows = pr.M > row_lo ? pr.M - row_lo : 0;
-    const int64_t nblk = (rows + 63) / 64;
-    w.has_bsum = true;
-    w.bsum = off;
-    off += align256((size_t)pr.B * pr.Hk * (nblk + 1) * pr.D * 4);
   }
   w.total = off;
   return w;
@@ -371,10 +388,9 @@ T* at(void* ws, size_t off) {
 }
 
 // Points the forward at its key-split partials when the plan splits.
-void apply_split(fas::FwdParams& p, const Problem& pr, const Workspace& w, void* ws,
-                 bool top_left) {
+void apply_split(fas::FwdParams& p, const Workspace& w, void* ws) {
   if (!w.has_split) return;
-  const SplitPlan sp = split_plan(pr, top_left);
+  const SplitPlan& sp = w.sp;
   p.nsplit = sp.nsplit;
   p.tps = sp.tps;
   p.Mpad = (int)sp.mpad;
@@ -406,7 +422,7 @@ int run_raw(const char* fn, int variant, const fas_attn_args* a, int64_t split, 
 
   // Attention output.
   fas::FwdParams p = fwd_params(a, pr, cross, fas::kFwdRows);
-  apply_split(p, pr, w, ws, cross);
+  apply_split(p, w, ws);
   if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, stream))) return rc;
   if (pr.M == 0) return zero_out3(fn, out, st, pr.B, pr.Hk, ncols, stream);
 
@@ -435,7 +451,8 @@ int run_raw(const char* fn, int variant, const fas_attn_args* a, int64_t split, 
 
 // Softmax-weight column sums (softmax col sum, cross softmax, buffered).
 int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t split, float* out,
-                const int64_t* st, void* ws, size_t ws_bytes, void* stream) {
+                const int64_t* st, void* ws, size_t ws_bytes, void* stream,
+                size_t budget = SIZE_MAX) {
   Problem pr;
   int rc;
   if ((rc = check_args(fn, a, &pr))) return rc;
@@ -445,12 +462,12 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
     return fail(FAS_ERR_INVALID, fn, "split %lld outside (0, %d]", (long long)split, pr.N);
   if ((rc = check_out3(fn, "sum output", out, st))) return rc;
   const int64_t ncols = ncols_of(variant, pr, split);
-  const Workspace w = layout(variant, pr, split);
+  const Workspace w = layout(variant, pr, split, budget);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
 
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   p.lse2 = at<float>(ws, w.lse);
-  if (!buffered) apply_split(p, pr, w, ws, false);
+  if (!buffered) apply_split(p, w, ws);
   if (buffered) {
     p.region = at<float>(ws, w.region);
     p.split = (int)split;
@@ -574,7 +591,7 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
     // scores-only kernel writes the masked scores in parallel over keys.
     fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
     rescale_dropout(p, a);
-    apply_split(p, pr, w, ws, false);
+    apply_split(p, w, ws);
     if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, stream))) return rc;
     return run_scores(fn, a, pr, scores, st, true, stream);
   }
@@ -619,7 +636,7 @@ int fas_attention_with_row_sum(const fas_attn_args* a, float* row_sum, const int
   const Workspace w = layout(FAS_VARIANT_ROW_SUM, pr, 0);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
-  apply_split(p, pr, w, ws, false);
+  apply_split(p, w, ws);
   p.aux = row_sum;
   p.sa0 = st[0];
   p.sa1 = st[1];
@@ -679,7 +696,7 @@ int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   rescale_dropout(p, a);
-  apply_split(p, pr, w, ws, false);
+  apply_split(p, w, ws);
   p.lse_ln = lse;
   p.sl0 = st[0];
   p.sl1 = st[1];

@@ -500,7 +500,14 @@ void fwd_kernel(const FwdParams p) {
             if (loader) {
               stage_tile((stage * 4 + wave) * TSZ, s, masked);
             } else {
-              // A wave reads back its own LDS writes in order: no barrier.
+              // The storer reads this tile back row-major in the next key
+              // tile (staged_pair), from other lanes of the same wave.  A
+              // wave's LDS accesses execute in issue order, so only the
+              // compiler must keep the order: the wave barrier keeps this
+              // iteration's read-back before these writes, and the step's
+              // closing lds_barrier (an asm with a memory clobber) keeps the
+              // writes before the next iteration's read-back.
+              __builtin_amdgcn_wave_barrier();
               stage_tile((8 + pwave) * TSZ, s, masked);
             }
           } else if (qrow < p.M) {

@@ -86,6 +86,13 @@ __global__ __launch_bounds__(64 * kScoresWaves) __attribute__((amdgpu_waves_per_
     }
     // Register r of block kb holds key kc + 32kb + 16*(r/8) + 8g + r%8.
     if (p.vec) {
+      // The wave's private stage is written in the MFMA layout and read back
+      // row-major by other lanes of the same wave.  A wave's LDS accesses
+      // execute in issue order, so a wave barrier (no instruction, an
+      // ordering point for the compiler) on each side of the hand-over is
+      // all the synchronisation this needs: before the read-back, and before
+      // the next chunk overwrites the stage.
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const int r = 32 * hh + c, row = row0 + r;
@@ -106,6 +113,7 @@ __global__ __launch_bounds__(64 * kScoresWaves) __attribute__((amdgpu_waves_per_
                       E::pack(v[6], v[7])};
           }
       }
+      __builtin_amdgcn_wave_barrier();
       // Row-major read-back: lane l takes unit l % 8 of rows l / 8 + 8i.
       const int u = lane & 7;
 #pragma unroll
