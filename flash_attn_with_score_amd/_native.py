@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -112,6 +112,8 @@ _SIGNATURES = {
         ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_with_softmax_col_sum": (
         ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
+    "fas_attention_with_softmax_col_sum_noalloc": (
+        ctypes.c_int, [_P(AttnArgs), ctypes.c_void_p, _I64x3, ctypes.c_void_p]),
     "fas_attention_cross_token_qk_sum": (
         ctypes.c_int, [_P(AttnArgs), ctypes.c_int64, ctypes.c_void_p, _I64x3, *_WS, ctypes.c_void_p]),
     "fas_attention_cross_token_softmax_sum": (

@@ -13,6 +13,7 @@
 #include <cstdio>
 #include <cstdint>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 
 #include "fas_launch.hpp"
@@ -519,6 +520,49 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   return FAS_OK;
 }
 
+// ------------------------------------------------- no-allocation scratch
+//
+// fas_attention_with_softmax_col_sum_noalloc takes its workspace from this
+// file-scope device array instead of a caller buffer, for callers that
+// cannot allocate.  Every GPU the library runs on holds its own copy for the
+// life of the process.  Host code must never pass `scratch` itself to a
+// kernel or copy: on the host the name is only a stand-in.  Its device
+// address is looked up once per device, with that device current, and kept
+// in g_scratch_ptr.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch, resolved on the first
+// call on each device.
+int scratch_of_current_device(const char* fn, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(fn, e);
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(FAS_ERR_UNSUPPORTED, fn, "device %d beyond the %d this build tracks", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return fail(FAS_ERR_HIP, fn, "hipGetSymbolAddress(scratch) on device %d failed: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FAS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -661,6 +705,26 @@ int fas_attention_with_softmax_col_sum(const fas_attn_args* a, float* col_sum, c
                                        void* ws, size_t ws_bytes, void* stream) {
   return run_softmax("fas_attention_with_softmax_col_sum", FAS_VARIANT_SOFTMAX_COL_SUM, a, 0,
                      col_sum, st, ws, ws_bytes, stream);
+}
+
+int fas_attention_with_softmax_col_sum_noalloc(const fas_attn_args* a, float* col_sum,
+                                               const int64_t st[3], void* stream) {
+  static const char* fn = "fas_attention_with_softmax_col_sum_noalloc";
+  Problem pr;
+  int rc;
+  if ((rc = check_shape(fn, a, &pr))) return rc;
+  // The layout is bounded by the scratch: a key split that would not fit
+  // takes fewer, longer splits (or none); what remains must fit.
+  const Workspace w = layout(FAS_VARIANT_SOFTMAX_COL_SUM, pr, 0, kNoAllocScratchBytes);
+  if (w.total > kNoAllocScratchBytes)
+    return fail(FAS_ERR_WORKSPACE, fn,
+                "needs %zu bytes of scratch, more than the %zu this entry point holds; call "
+                "fas_attention_with_softmax_col_sum with a caller workspace instead",
+                w.total, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_of_current_device(fn, &ws))) return rc;
+  return run_softmax(fn, FAS_VARIANT_SOFTMAX_COL_SUM, a, 0, col_sum, st, ws, kNoAllocScratchBytes,
+                     stream, kNoAllocScratchBytes);
 }
 
 int fas_attention_cross_token_qk_sum(const fas_attn_args* a, int64_t split, float* cross,

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FAS_ABI_VERSION 5
+#define FAS_ABI_VERSION 6
 
 typedef enum fas_dtype {
   FAS_DTYPE_F16 = 0,
@@ -171,6 +171,23 @@ int fas_attention_with_col_sum_sequential(const fas_attn_args* a, float* col_sum
 int fas_attention_with_softmax_col_sum(const fas_attn_args* a, float* col_sum,
                                        const int64_t col_sum_stride[3], void* workspace,
                                        size_t workspace_bytes, void* stream);
+
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same computation and kernels as
+ * fas_attention_with_softmax_col_sum, with the workspace taken from a
+ * file-scope device array of the library instead of a caller buffer.  The
+ * caller still passes the inputs and outputs; nothing is allocated or freed,
+ * here or in any library routine this call makes.
+ * Limits: the array holds 64 MiB per GPU (B*Hq*M*4 bytes of row normalizers,
+ * + B*Hq*N*4 of group partials when Hq > Hk, + key-split partials, which
+ * shrink to fit); larger problems return FAS_ERR_WORKSPACE.  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other host threads) race and must be serialised by the caller.
+ * No part of the array needs to start at zero; each call writes what it
+ * reads. */
+int fas_attention_with_softmax_col_sum_noalloc(const fas_attn_args* a, float* col_sum,
+                                               const int64_t col_sum_stride[3], void* stream);
 
 /* Replaces attention_cross_token_qk_sum.py:255-408 (+ kernel :17-252):
  * cross is (B, Hk, split) fp32, sum over queries i >= split of (q.k)*sm_scale

@@ -40,7 +40,7 @@ def header_functions():
 
 
 def test_library_loads_with_abi_version(lib):
-    assert lib.fas_abi_version() == _native.ABI_VERSION == 5
+    assert lib.fas_abi_version() == _native.ABI_VERSION == 6
 
 
 def test_exports_match_header(lib):
