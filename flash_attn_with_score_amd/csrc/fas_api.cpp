@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdarg>
@@ -67,7 +68,28 @@ uint32_t slice_bytes(int64_t rows, int64_t row_stride, int64_t D) {
 struct Problem {
   int B, H, Hk, G, M, N, D, dtype, causal;
   float sm_scale;
+  int pack;  // query heads per forward workgroup (GQA packing): G, or 1
 };
+
+// Bytes a 16-bit (B, H, L, D) tensor spans over `heads` consecutive heads of
+// one batch entry, including the tile overhang the kernels may address past
+// the last row.
+int64_t head_span_bytes(const int64_t* st, int64_t heads, int64_t rows) {
+  return ((heads - 1) * st[1] + (rows + 512) * st[2]) * 2;
+}
+
+// GQA packing: a forward workgroup serves all G query heads of a KV head
+// when the G heads of q and out can be addressed with 32-bit offsets from
+// the first (the kernels mark invalid rows with offset 2^31).
+int choose_pack(const fas_attn_args* a, int G, int M) {
+  // Launches with dropout keep one head per workgroup (no packed dropout
+  // instances are built).
+  if (G <= 1 || a->dropout_p > 0.f) return 1;
+  if (head_span_bytes(a->q_stride, G, M) >= kMaxSliceBytes ||
+      head_span_bytes(a->out_stride, G, M) >= kMaxSliceBytes)
+    return 1;
+  return G;
+}
 
 // Sizes, dtype and flags only (no pointers): enough to size a workspace.
 int check_shape(const char* fn, const fas_attn_args* a, Problem* pr) {
@@ -103,6 +125,7 @@ int check_shape(const char* fn, const fas_attn_args* a, Problem* pr) {
   pr->dtype = a->dtype;
   pr->causal = a->causal;
   pr->sm_scale = a->sm_scale;
+  pr->pack = choose_pack(a, pr->G, pr->M);
   return FAS_OK;
 }
 
@@ -179,8 +202,9 @@ fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_le
   p.sk0 = a->k_stride[0]; p.sk1 = a->k_stride[1]; p.sk2 = a->k_stride[2];
   p.sv0 = a->v_stride[0]; p.sv1 = a->v_stride[1]; p.sv2 = a->v_stride[2];
   p.so0 = a->out_stride[0]; p.so1 = a->out_stride[1]; p.so2 = a->out_stride[2];
-  p.q_bytes = slice_bytes(pr.M, p.sq2, pr.D);
-  p.o_bytes = slice_bytes(pr.M, p.so2, pr.D);
+  // q and out are addressed from the first head of a packed group.
+  p.q_bytes = slice_bytes(pr.M, p.sq2, pr.D) + (uint32_t)((pr.pack - 1) * p.sq1 * 2);
+  p.o_bytes = slice_bytes(pr.M, p.so2, pr.D) + (uint32_t)((pr.pack - 1) * p.so1 * 2);
   p.k_bytes = slice_bytes(pr.N, p.sk2, pr.D);
   p.v_bytes = slice_bytes(pr.N, p.sv2, pr.D);
   p.qneg = pr.sm_scale < 0.f ? 0x80008000u : 0u;
@@ -191,7 +215,9 @@ fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_le
   p.N = pr.N;
   p.causal = pr.causal;
   p.causal_off = top_left ? 0 : pr.N - pr.M;
-  p.nrb = (pr.M + rows_per_block - 1) / rows_per_block;
+  p.pack = pr.pack;
+  p.pack_shift = pr.pack == 1 ? 0 : pr.pack == 2 ? 1 : pr.pack == 4 ? 2 : pr.pack == 8 ? 3 : -1;
+  p.nrb = (int)(((int64_t)pr.M * pr.pack + rows_per_block - 1) / rows_per_block);
   p.nsplit = 1;
   p.sm_scale = std::fabs(pr.sm_scale);
   p.qk_scale = qk_scale_of(pr.sm_scale);
@@ -254,12 +280,13 @@ size_t split_bytes(const Problem& pr, const SplitPlan& sp) {
 SplitPlan split_plan(const Problem& pr, bool top_left, int64_t max_wgs = 255,
                      size_t max_bytes = SIZE_MAX) {
   SplitPlan sp;
-  const int64_t nrb = ((int64_t)pr.M + fas::kFwdRows - 1) / fas::kFwdRows;
-  const int64_t wgs = (int64_t)pr.B * pr.H * nrb;
+  // Virtual row blocks of each group of pack heads (the forward's grid).
+  const int64_t nrb = ((int64_t)pr.M * pr.pack + fas::kFwdRows - 1) / fas::kFwdRows;
+  const int64_t wgs = (int64_t)pr.B * (pr.H / pr.pack) * nrb;
   if (wgs == 0 || wgs > max_wgs) return sp;
   const int64_t off = top_left ? 0 : (int64_t)pr.N - pr.M;
   int64_t hi = pr.N;
-  if (pr.causal) hi = std::min<int64_t>(pr.N, std::max<int64_t>(0, off + nrb * fas::kFwdRows));
+  if (pr.causal) hi = std::min<int64_t>(pr.N, std::max<int64_t>(0, off + pr.M));
   const int64_t nt = (hi + 63) / 64;
   for (int64_t want = std::min<int64_t>((512 + wgs - 1) / wgs, nt / 8); want >= 2; --want) {
     const int64_t tps = (nt + want - 1) / want;
@@ -268,7 +295,8 @@ SplitPlan split_plan(const Problem& pr, bool top_left, int64_t max_wgs = 255,
     SplitPlan c;
     c.nsplit = (int)ns;
     c.tps = (int)tps;
-    c.mpad = nrb * fas::kFwdRows;
+    // Partials are indexed by (head, split, position): M rounded up.
+    c.mpad = (((int64_t)pr.M + fas::kFwdRows - 1) / fas::kFwdRows) * fas::kFwdRows;
     if (split_bytes(pr, c) <= max_bytes) return c;
   }
   return sp;
@@ -580,7 +608,16 @@ size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM ||
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED;
   if (has_split && !(split > 0 && split <= pr.N)) return (size_t)-1;
-  return layout(variant, pr, has_split ? split : 0).total;
+  // The key-split plan depends on the GQA packing, which a launch picks
+  // from the strides; the size covers both choices, so a query made with
+  // placeholder strides still suffices.
+  size_t total = 0;
+  for (int pk : {1, pr.G}) {
+    Problem q = pr;
+    q.pack = pk;
+    total = std::max(total, layout(variant, q, has_split ? split : 0).total);
+  }
+  return total;
 }
 
 static int check_scores_out(const char* fn, const void* scores, const int64_t* st) {
@@ -640,7 +677,15 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
     return run_scores(fn, a, pr, scores, st, true, stream);
   }
   const int bm = fas::kFwdRows;
-  fas::FwdParams p = fwd_params(a, pr, false, bm);
+  // The score writer packs 2, 4 or 8 heads (its store layout keeps a lane's
+  // head fixed) and addresses their score rows from the first head's, below
+  // offset 2^31; otherwise each workgroup takes one head.
+  Problem pw = pr;
+  if (pw.pack > 1 &&
+      ((pw.pack != 2 && pw.pack != 4 && pw.pack != 8) ||
+       ((int64_t)(pw.pack - 1) * st[1] + (int64_t)(bm / pw.pack + 2) * st[2]) * 2 >= kMaxSliceBytes))
+    pw.pack = 1;
+  fas::FwdParams p = fwd_params(a, pw, false, bm);
   rescale_dropout(p, a);
   p.scores = static_cast<uint16_t*>(scores);
   p.ss0 = st[0];

@@ -56,19 +56,29 @@
 
 namespace fas {
 
-// Maps a workgroup id to (row block, batch*head).  Workgroups are dealt to
-// the 8 XCDs round-robin by id; when B*H is a multiple of 8, each XCD gets a
-// contiguous set of heads (one KV group stays in one L2) and, within it,
-// row blocks in descending length for causal masks.
-__device__ __forceinline__ void map_block(int bid, int nrb, int BH, bool causal, int& rb,
-                                          int& bh) {
-  if ((BH & 7) == 0) {
-    const int x = bid & 7, s = bid >> 3, per = BH >> 3;
-    bh = x * per + s % per;
+// Maps a workgroup id to (row block, group), a group being one batch entry's
+// `pack` query heads of one KV head.  Workgroups are dealt to the 8 XCDs
+// round-robin by id, and each XCD has its own L2, so the mapping keeps a
+// group's row blocks on as few XCDs as it can:
+//  * ngroups a multiple of 8: each XCD gets a contiguous set of groups;
+//  * ngroups 1, 2 or 4 (and nrb a multiple of 8/ngroups): each group gets
+//    8/ngroups XCDs, which take its row blocks in turn;
+//  * otherwise groups are dealt round-robin.
+// Within an XCD, row blocks run in descending length for causal masks.
+__device__ __forceinline__ void map_block(int bid, int nrb, int ngroups, bool causal, int& rb,
+                                          int& grp) {
+  const int x = bid & 7, s = bid >> 3;
+  if ((ngroups & 7) == 0) {
+    const int per = ngroups >> 3;
+    grp = x * per + s % per;
     rb = s / per;
+  } else if ((8 % ngroups) == 0 && nrb % (8 / ngroups) == 0) {
+    const int k = 8 / ngroups;
+    grp = x / k;
+    rb = s * k + x % k;
   } else {
-    bh = bid % BH;
-    rb = bid / BH;
+    grp = bid % ngroups;
+    rb = bid / ngroups;
   }
   if (causal) rb = nrb - 1 - rb;
 }
@@ -76,58 +86,89 @@ __device__ __forceinline__ void map_block(int bid, int nrb, int BH, bool causal,
 // Byte offset that every buffer access treats as out of range (dropped).
 constexpr uint32_t kOffNone = 0x80000000u;
 
+// Score-row addressing for the score writer's stores.  A store instruction
+// covers 8 consecutive virtual rows V..V+7 (V a multiple of 8), lane l
+// writing row V + l/8.  The score writer packs 1, 2, 4 or 8 heads (shift =
+// log2 pack), so the lane's head (l/8) % pack is the same in every such
+// group and its position is V/pack + (l/8 >> shift): one per-lane offset
+// (lane_off, which also holds the lane's 16-byte chunk) plus a uniform
+// (V/pack - pos0) * row_bytes, from a buffer based at position pos0 of the
+// group's first head.  Rows past M: with one head they fall outside the
+// buffer's extent; with several they would land in the next head's rows,
+// so the lane's position (lpos) is checked against a uniform limit.
+struct RowGeom {
+  int shift = 0, M = 0, pos0 = 0;
+  uint32_t row_bytes = 0, head_bytes = 0;
+  __device__ __forceinline__ uint32_t lane_off(int lane) const {
+    const int lrow = lane >> 3;
+    return (uint32_t)(lrow & ((1 << shift) - 1)) * head_bytes + (uint32_t)(lrow >> shift) * row_bytes +
+           (uint32_t)(16 * (lane & 7));
+  }
+  // Uniform part of the offset of the 8-row group starting at virtual row V.
+  __device__ __forceinline__ uint32_t group_off(int V) const {
+    return (uint32_t)((V >> shift) - pos0) * row_bytes;
+  }
+};
+
 // Zero writer for the never-computed causal part of two 32-row rectangles of
-// a row block: rows [ra, ra + 32) x keys [za, N) and rows [rb, rb + 32) x
-// keys [zb, N) (row numbers relative to the block, za and zb multiples of
-// 64).  Each store covers 8 rows x 64 keys: eight full 128-byte row
-// segments, lane l writing row l / 8, 16-byte chunk l % 8.  The writer walks
-// eight runs -- the 8-row groups of a, then those of b -- each left to right
-// in batches of eight 64-key blocks, so the HBM sees long runs along each row:
-// measured on the MI355X, writing a 1 GiB score matrix this way runs at
-// 6.2 TB/s against 3.9 TB/s when every store moves to other rows.
+// a row block: virtual rows [ra, ra + 32) x keys [za, N) and [rb, rb + 32) x
+// keys [zb, N) (row numbers absolute, za and zb multiples of 64).  Each
+// store covers 8 rows x 64 keys: eight full 128-byte row segments, lane l
+// writing row l / 8, 16-byte chunk l % 8.  The writer walks eight runs --
+// the 8-row groups of a, then those of b -- each left to right in batches of
+// eight 64-key blocks, so the HBM sees long runs along each row: measured on
+// the MI355X, writing a 1 GiB score matrix this way runs at 6.2 TB/s
+// against 3.9 TB/s when every store moves to other rows.
 // Inside the key loop only full batches are written: eight blocks that lie
 // wholly below key N.  Store i of a batch takes the lane's row offset as
-// voffset (rows past the block's extent fall outside the buffer and are
-// dropped), the batch's key offset as the wave-uniform scalar offset and
-// 128*i as the immediate, so a batch costs one vector select and scalar
-// bookkeeping.  The remaining blocks of each run (fewer than eight, the last
-// one possibly cut by N) are written by tail() after the loop.
+// voffset (kOffNone for rows past M), the batch's key offset as the
+// wave-uniform scalar offset and 128*i as the immediate, so a batch costs
+// one vector select and scalar bookkeeping.  The remaining blocks of each
+// run (fewer than eight, the last one possibly cut by N) are written by
+// tail() after the loop.
+template <bool PACK>
 struct ZeroRuns {
   int run = 8;          // current run, 0-3 in a, 4-7 in b, 8 = no full batch left
   int nb = 0;           // full batches left in the current run
   uint32_t koff = 0;    // byte offset of the batch's first key
-  uint32_t roff = 0;    // byte offset of the run's first row
+  uint32_t roff = 0;    // uniform offset of the current run's 8-row group
+  int lim = 0;          // PACK: positions of the current run's group below M
   int ra = 0, rb = 0, za = 0, zb = 0, ca = 0, cb = 0, N = 0;
-  uint32_t row_bytes = 0;
+  uint32_t lane_off = 0;  // the lane's row in the group and its chunk
+  int lpos = 0;           // PACK: the lane's position within the group
+  RowGeom geo;
 
-  // 64-key blocks per row of a rectangle starting at key z with rows_valid
-  // rows inside the matrix, and how many full batches they hold.
-  __device__ __forceinline__ static int blocks(int N, int z, int rows_valid) {
-    return (rows_valid > 0 && N > z) ? (N - z + 63) >> 6 : 0;
+  // 64-key blocks per row of a rectangle starting at key z whose first row
+  // lies inside the matrix, and how many full batches they hold.
+  __device__ __forceinline__ static int blocks(int N, int z, bool rows_valid) {
+    return (rows_valid && N > z) ? (N - z + 63) >> 6 : 0;
   }
   __device__ __forceinline__ static int full_batches(int N, int c) {
     return c > 0 ? (c - ((N & 63) != 0 ? 1 : 0)) >> 3 : 0;
   }
-  __device__ __forceinline__ void init(int ra_, int za_, int rows_a, int rb_, int zb_, int rows_b,
-                                       int N_, int ss2) {
-    ra = ra_; rb = rb_; za = za_; zb = zb_; N = N_;
-    row_bytes = (uint32_t)ss2 * 2u;
-    ca = blocks(N, za, rows_a);
-    cb = blocks(N, zb, rows_b);
+  __device__ __forceinline__ void init(int ra_, int za_, int rb_, int zb_, int N_, int lane,
+                                       const RowGeom& g) {
+    ra = ra_; rb = rb_; za = za_; zb = zb_; N = N_; geo = g;
+    lane_off = g.lane_off(lane);
+    lpos = (lane >> 3) >> g.shift;
+    ca = blocks(N, za, (ra >> g.shift) < g.M);
+    cb = blocks(N, zb, (rb >> g.shift) < g.M);
     start(full_batches(N, ca) > 0 ? 0 : (full_batches(N, cb) > 0 ? 4 : 8));
   }
+  __device__ __forceinline__ int run_first(int r) const { return (r < 4 ? ra : rb) + 8 * (r & 3); }
   __device__ __forceinline__ void start(int r) {
     run = r;
     const bool in_a = r < 4;
     nb = r < 8 ? full_batches(N, in_a ? ca : cb) : 0;
     koff = (uint32_t)(in_a ? za : zb) * 2u;
-    roff = (uint32_t)((in_a ? ra : rb) + 8 * (r & 3)) * row_bytes;
+    roff = geo.group_off(run_first(r & 7));
+    lim = geo.M - (run_first(r & 7) >> geo.shift);
   }
   __device__ __forceinline__ bool pending() const { return run < 8; }
   // voffset of store 0 of the current batch (kOffNone once no full batch is
-  // left); store i adds 128*i.
-  __device__ __forceinline__ uint32_t vbase(uint32_t lane_off) const {
-    return run < 8 ? lane_off + roff : kOffNone;
+  // left, or for a row past M); store i adds 128*i.
+  __device__ __forceinline__ uint32_t vbase() const {
+    return run < 8 && (!PACK || lpos < lim) ? roff + lane_off : kOffNone;
   }
   __device__ __forceinline__ void advance() {
     koff += 1024u;
@@ -136,14 +177,15 @@ struct ZeroRuns {
   }
   // Blocks of every run past its full batches, masked at key N.
   template <class Store>
-  __device__ __forceinline__ void tail(uint32_t lane_off, int lane_key, Store&& store) const {
+  __device__ __forceinline__ void tail(int lane_key, Store&& store) const {
     for (int r = 0; r < 8; ++r) {
       const bool in_a = r < 4;
       const int c = in_a ? ca : cb, z = in_a ? za : zb;
-      const uint32_t ro = (uint32_t)((in_a ? ra : rb) + 8 * (r & 3)) * row_bytes;
+      const uint32_t ro = geo.group_off(run_first(r));
+      const bool row_ok = !PACK || lpos < geo.M - (run_first(r) >> geo.shift);
       for (int kb = 8 * full_batches(N, c); kb < c; ++kb) {
         const int k = z + 64 * kb;
-        store(lane_key < N - k ? lane_off + ro : kOffNone, (uint32_t)k * 2u);
+        store(lane_key < N - k && row_ok ? ro + lane_off : kOffNone, (uint32_t)k * 2u);
       }
     }
   }
@@ -177,10 +219,14 @@ __device__ __forceinline__ void sched_score_tile() {
   if (NST > KS) __builtin_amdgcn_sched_group_barrier(0x040, NST > KS ? NST - KS : 1, 0);
 }
 
-template <class E, int D, int MODE, int NW, bool DROP>
+// PACK: GQA packing (p.pack query heads per workgroup, per-lane heads and
+// positions); without it the workgroup's rows are one head's and every
+// per-lane head offset folds away at compile time.
+template <class E, int D, int MODE, int NW, bool DROP, bool PACK>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(const FwdParams p) {
   static_assert(MODE != kFwdScores || NW == 8, "the score writer uses 8 waves");
+  const int pack = PACK ? p.pack : 1;
   constexpr int KS = D / 16;               // MFMA k-steps over the head dim
   constexpr int DB = (D + 31) / 32;        // 32-dim blocks of O^T
   constexpr int BM = 32 * NW;
@@ -211,32 +257,51 @@ void fwd_kernel(const FwdParams p) {
   // Split over keys: the plain and row-sum modes may give a row block to
   // nsplit workgroups, each over its own share of the key tiles.
   constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdRowSum;
-  int rb, bh, split = 0;
+  int rb, grp, split = 0;
   {
     int bid = blockIdx.x;
     if constexpr (kCanSplit) {
       split = bid % p.nsplit;
       bid /= p.nsplit;
     }
-    map_block(bid, p.nrb, p.B * p.H, p.causal != 0, rb, bh);
+    map_block(bid, p.nrb, p.B * p.H / pack, p.causal != 0, rb, grp);
   }
-  const int h = bh % p.H, b = bh / p.H, hk = h / p.G;
+  // The group's heads h0 .. h0 + pack - 1 share KV head hk.  Virtual row
+  // v = pos * pack + j is position pos of head h0 + j; a lane owns one
+  // virtual row, so its position and head are per-lane values.
+  const int gpb = p.H / pack;  // groups per batch entry
+  const int b = grp / gpb, h0 = (grp - b * gpb) * pack, hk = h0 / p.G;
   const int row0 = rb * BM;
   const int wrow0 = row0 + 32 * wave;
-  const int qrow = wrow0 + c;
+  const int vrow = wrow0 + c;
+  const int qpos = vrow / pack;
+  const int qh = h0 + (vrow - qpos * pack);
+  const int bh = b * p.H + qh;
+  const bool row_ok = qpos < p.M;
+  // First and last position of a run of virtual rows [r, r + n).
+  auto pos_lo = [&](int r) { return r / pack; };
+  auto pos_hi = [&](int r, int n) { return min(p.M - 1, (r + n - 1) / pack); };
 
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h0 * p.sq1, p.q_bytes);
   const i32x4 wk = make_rsrc_words(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
   const i32x4 wv = make_rsrc_words(p.v + b * p.sv0 + hk * p.sv1, p.v_bytes);
   const uint32_t kv_base = lds_addr(&kv[0][0][0]);
+  // Byte offsets of the lane's q and out rows (kOffNone past M: q reads
+  // zeros, out stores are dropped).
+  const uint32_t qoff = row_ok ? (uint32_t)(((int64_t)(qh - h0) * p.sq1 + (int64_t)qpos * p.sq2) * 2)
+                               : kOffNone;
+  const uint32_t ooff = row_ok ? (uint32_t)(((int64_t)(qh - h0) * p.so1 + (int64_t)qpos * p.so2) * 2)
+                               : kOffNone;
 
-  // Key range of a wave starting at row r: tiles [0, wt(r)) are computed,
-  // tiles [0, tf(r)) need no mask.
+  // Key range of a wave starting at virtual row r: tiles [0, wt(r)) are
+  // computed (up to its last position's diagonal), tiles [0, tfull) need no
+  // mask.
   auto wtiles_of = [&](int r) {
-    const int whi = p.causal ? min(p.N, max(0, p.causal_off + r + 32)) : p.N;
+    if (pos_lo(r) >= p.M) return 0;  // every row of the wave lies past M
+    const int whi = p.causal ? min(p.N, max(0, p.causal_off + pos_hi(r, 32) + 1)) : p.N;
     return (whi + BN - 1) / BN;
   };
-  const int hi = p.causal ? min(p.N, max(0, p.causal_off + row0 + BM)) : p.N;
+  const int hi = p.causal ? min(p.N, max(0, p.causal_off + pos_hi(row0, BM) + 1)) : p.N;
   const int ntiles = (hi + BN - 1) / BN;
   // This workgroup's key tiles [t_begin, t_end): all of them, or one split's
   // share (possibly none).
@@ -249,13 +314,14 @@ void fwd_kernel(const FwdParams p) {
   }
   const int wtiles = wtiles_of(wrow0);
   int tfull = p.N / BN;
-  if (p.causal) tfull = min(tfull, max(0, p.causal_off + wrow0 + 1) / BN);
+  if (p.causal) tfull = min(tfull, max(0, p.causal_off + pos_lo(wrow0) + 1) / BN);
 
-  // Q (B operand of S^T = K Q^T): lane holds Q[qrow][16ks + 8g, +8).
+  // Q (B operand of S^T = K Q^T): lane holds Q[qpos][16ks + 8g, +8) of
+  // head qh.
   u32x4 qreg[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks)
-    qreg[ks] = buf_load16(rq, (uint32_t)((qrow * p.sq2 + 16 * ks + 8 * g) * 2)) ^ p.qneg;
+    qreg[ks] = buf_load16(rq, qoff + (uint32_t)((16 * ks + 8 * g) * 2)) ^ p.qneg;
 
   // Tile t -> LDS stage: block q of K (and of V) is rows [q*RPB, +RPB);
   // lane l fills physical chunk l % CPR of row q*RPB + l / CPR.
@@ -283,28 +349,40 @@ void fwd_kernel(const FwdParams p) {
   const bool storer = vec && !loader;
   const int pwave = wave - 4;  // the loader wave a storer serves
   const int pwtiles = kSplit ? wtiles_of(row0 + 32 * pwave) : 0;
-  const int ss2 = (int)p.ss2;
   // Lane (row l/8, chunk l%8) of an 8-row x 128-byte store.
   const int lane_key = 8 * (lane & 7);
-  const uint32_t lane_off = (uint32_t)(((lane >> 3) * ss2 + lane_key) * 2);
   __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scores, 0);
   __amdgpu_buffer_rsrc_t rz = rs;
-  ZeroRuns zr;
+  ZeroRuns<PACK> zr;
+  // Score rows (RowGeom): the storer's stores address rows 8i + l/8 of a
+  // 32-row wave tile through the lane's fixed offset plus a uniform part.
+  const int sshift = PACK ? p.pack_shift : 0;
+  RowGeom gs;
+  uint32_t lane_off = 0;
+  const int lpos = (lane >> 3) >> sshift;
   if constexpr (MODE == kFwdScores) {
-    const int64_t base = b * p.ss0 + h * p.ss1 + (int64_t)row0 * p.ss2;
-    const int rows = max(0, min(BM, p.M - row0));
-    // Extents pass through readfirstlane: the clamps may be computed on the
-    // vector ALU, and a descriptor in VGPRs costs a loop around every store.
-    rs = make_rsrc(p.scores + base, __builtin_amdgcn_readfirstlane((uint32_t)(rows * p.ss2 * 2)));
-    // Zeros of the mirror row block; rows past M fall outside rz.
+    // rs covers the group's heads from the block's first position, rz the
+    // same from the mirror block's first position.  The extents pass
+    // through readfirstlane: they may be computed on the vector ALU, and a
+    // descriptor in VGPRs costs a loop around every store.
+    const uint32_t hspan = (uint32_t)((pack - 1) * p.ss1 * 2);
+    const int pos0 = min(p.M, pos_lo(row0));
+    const int pos1 = min(p.M, pos_lo(row0 + BM - 1) + 1);
+    rs = make_rsrc(p.scores + b * p.ss0 + h0 * p.ss1 + (int64_t)pos0 * p.ss2,
+                   __builtin_amdgcn_readfirstlane(hspan + (uint32_t)((pos1 - pos0) * p.ss2 * 2)));
+    gs = RowGeom{sshift, p.M, pos0, (uint32_t)(p.ss2 * 2), (uint32_t)(p.ss1 * 2)};
+    lane_off = gs.lane_off(lane);
+    // Zeros of the mirror row block.
     const int mrow0 = (p.nrb - 1 - rb) * BM;
-    const int mrows = max(0, min(BM, p.M - mrow0));
-    rz = make_rsrc(p.scores + b * p.ss0 + h * p.ss1 + (int64_t)mrow0 * p.ss2,
-                   __builtin_amdgcn_readfirstlane((uint32_t)(mrows * p.ss2 * 2)));
+    const int mpos0 = min(p.M, pos_lo(mrow0));
+    const int mpos1 = min(p.M, pos_lo(mrow0 + BM - 1) + 1);
+    rz = make_rsrc(p.scores + b * p.ss0 + h0 * p.ss1 + (int64_t)mpos0 * p.ss2,
+                   __builtin_amdgcn_readfirstlane(hspan + (uint32_t)((mpos1 - mpos0) * p.ss2 * 2)));
     if (storer) {
+      RowGeom gz = gs;
+      gz.pos0 = mpos0;
       const int wa = wtiles_of(mrow0 + 32 * wave), wb = wtiles_of(mrow0 + 32 * pwave);
-      zr.init(32 * wave, wa * BN, p.M - (mrow0 + 32 * wave), 32 * pwave, wb * BN,
-              p.M - (mrow0 + 32 * pwave), p.N, ss2);
+      zr.init(mrow0 + 32 * wave, wa * BN, mrow0 + 32 * pwave, wb * BN, p.N, lane, gz);
     }
   }
   // Staged score tile: row r (32 rows), 16-byte chunk ch (8 per row) at
@@ -339,16 +417,20 @@ void fwd_kernel(const FwdParams p) {
       w[i] = stg[base + r * 8 + (ch ^ ((r >> 1) & 7))];
     }
   };
-  auto staged_offsets = [&](int rbase, int k0, bool valid, uint32_t (&o)[4])
+  // Rows 8i + l/8 of the wave tile starting at virtual row T, keys k0..
+  auto staged_offsets = [&](int T, int k0, bool valid, uint32_t (&o)[4])
                             __attribute__((always_inline)) {
     const bool ok = valid && k0 + lane_key < p.N;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      o[i] = ok ? (uint32_t)(((rbase + 8 * i) * ss2 + k0) * 2) + lane_off : kOffNone;
+    for (int i = 0; i < 4; ++i) {
+      const int V = T + 8 * i;
+      const bool row_ok = !PACK || lpos < p.M - (V >> sshift);
+      o[i] = ok && row_ok ? gs.group_off(V) + (uint32_t)(k0 * 2) + lane_off : kOffNone;
+    }
   };
   // One batch of kZero = 8 zero stores.
   auto zero_batch = [&]() __attribute__((always_inline)) {
-    const uint32_t vb = zr.vbase(lane_off);
+    const uint32_t vb = zr.vbase();
 #pragma unroll
     for (int i = 0; i < kZero; ++i)
       buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rz, vb + 128u * (uint32_t)i, zr.koff);
@@ -361,8 +443,8 @@ void fwd_kernel(const FwdParams p) {
     uint32_t op[4], oo[4];
     read_staged(((t & 1) * 4 + pwave) * TSZ, wp);
     read_staged((8 + pwave) * TSZ, wo);
-    staged_offsets(32 * pwave, t * BN, t >= 0 && t < pwtiles, op);
-    staged_offsets(32 * wave, t * BN, t >= 0 && t < wtiles, oo);
+    staged_offsets(row0 + 32 * pwave, t * BN, t >= 0 && t < pwtiles, op);
+    staged_offsets(row0 + 32 * wave, t * BN, t >= 0 && t < wtiles, oo);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       w[i] = wp[i];
@@ -426,7 +508,7 @@ void fwd_kernel(const FwdParams p) {
   // Dropout (DROP instances): zero the packed weights of dropped elements
   // after the row sum has taken them (attention_with_scores.py:169-176).
   // Weight e of pb[cs] is key k0 + 16cs + 8g + e of this lane's row.
-  const uint32_t drow = ((uint32_t)bh * (uint32_t)p.M + (uint32_t)qrow) * (uint32_t)p.drop.n;
+  const uint32_t drow = ((uint32_t)bh * (uint32_t)p.M + (uint32_t)qpos) * (uint32_t)p.drop.n;
   auto drop_p = [&](u32x4 (&pb)[4], int k0) __attribute__((always_inline)) {
 #pragma unroll
     for (int cs = 0; cs < 4; ++cs)
@@ -490,7 +572,7 @@ void fwd_kernel(const FwdParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = k0 + 32 * kb + acc_row(r, g);
-              const bool ok = key < p.N && (!p.causal || p.causal_off + qrow >= key);
+              const bool ok = key < p.N && (!p.causal || p.causal_off + qpos >= key);
               if (!ok) s[kb][r] = neg_inf();
             }
         }
@@ -510,15 +592,15 @@ void fwd_kernel(const FwdParams p) {
               __builtin_amdgcn_wave_barrier();
               stage_tile((8 + pwave) * TSZ, s, masked);
             }
-          } else if (qrow < p.M) {
-            uint16_t* srow = p.scores + b * p.ss0 + h * p.ss1 + (int64_t)qrow * p.ss2;
+          } else if (row_ok) {
+            uint16_t* sr = p.scores + b * p.ss0 + qh * p.ss1 + (int64_t)qpos * p.ss2;
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
               for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 32 * kb + acc_row(r, g);
                 const float x = s[kb][r];
-                if (key < p.N) srow[key] = E::cvt(x == neg_inf() ? 0.f : x * p.sm_scale);
+                if (key < p.N) sr[key] = E::cvt(x == neg_inf() ? 0.f : x * p.sm_scale);
               }
           }
         }
@@ -529,8 +611,8 @@ void fwd_kernel(const FwdParams p) {
             for (int r = 0; r < 16; ++r) rsum += s[kb][r] == neg_inf() ? 0.f : s[kb][r];
         }
         if constexpr (MODE == kFwdRegion) {
-          if (qrow >= p.split && qrow < p.M && k0 < p.split) {
-            float* brow = p.region + ((int64_t)bh * (p.M - p.split) + (qrow - p.split)) * p.split;
+          if (qpos >= p.split && row_ok && k0 < p.split) {
+            float* brow = p.region + ((int64_t)bh * (p.M - p.split) + (qpos - p.split)) * p.split;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const f32x16& sv = s[j >> 1];
@@ -650,17 +732,17 @@ void fwd_kernel(const FwdParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
       while (zr.pending()) zero_batch();
-      zr.tail(lane_off, lane_key, [&](uint32_t vo, uint32_t so) {
+      zr.tail(lane_key, [&](uint32_t vo, uint32_t so) {
         buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rz, vo, so);
       });
     }
     if (!vec) {  // element-wise zero triangle for unaligned rows
       const int z0 = min(p.N, wtiles * BN);
       for (int rr = 0; rr < 32; ++rr) {
-        const int row = wrow0 + rr;
-        if (row >= p.M) break;
-        uint16_t* srow = p.scores + b * p.ss0 + h * p.ss1 + (int64_t)row * p.ss2;
-        for (int key = z0 + lane; key < p.N; key += 64) srow[key] = 0;
+        const int v = wrow0 + rr, pos = v / pack;
+        if (pos >= p.M) break;
+        uint16_t* sr = p.scores + b * p.ss0 + (h0 + v - pos * pack) * p.ss1 + (int64_t)pos * p.ss2;
+        for (int key = z0 + lane; key < p.N; key += 64) sr[key] = 0;
       }
     }
   }
@@ -672,8 +754,8 @@ void fwd_kernel(const FwdParams p) {
       // One split's share: unnormalised O, offset and weight sum (and the
       // raw row sum) in fp32 for fwd_combine_kernel.
       const float r_tot = MODE == kFwdRowSum ? xor32_add(rsum) : 0.f;
-      if (qrow < p.M) {
-        const int64_t prow = ((int64_t)bh * p.nsplit + split) * p.Mpad + qrow;
+      if (row_ok) {
+        const int64_t prow = ((int64_t)bh * p.nsplit + split) * p.Mpad + qpos;
         float* po = p.part_o + prow * D;
 #pragma unroll
         for (int db = 0; db < DB; ++db)
@@ -699,7 +781,7 @@ void fwd_kernel(const FwdParams p) {
   }
   float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if constexpr (DROP) inv *= p.drop.scale;
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.o + b * p.so0 + h * p.so1, p.o_bytes);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.o + b * p.so0 + h0 * p.so1, p.o_bytes);
 #pragma unroll
   for (int db = 0; db < DB; ++db)
 #pragma unroll
@@ -712,21 +794,21 @@ void fwd_kernel(const FwdParams p) {
                          E::pack(o[r0 + 2] * inv, o[r0 + 3] * inv),
                          E::pack(o[r0 + 4] * inv, o[r0 + 5] * inv),
                          E::pack(o[r0 + 6] * inv, o[r0 + 7] * inv)};
-        buf_store16(w, ro, (uint32_t)((qrow * p.so2 + d0) * 2));
+        buf_store16(w, ro, ooff == kOffNone ? kOffNone : ooff + (uint32_t)(d0 * 2));
       }
     }
-  if (g == 0 && qrow < p.M) {
+  if (g == 0 && row_ok) {
     const float lse2 = m_ref * p.qk_scale + log2f_fast(l_tot);
-    if (p.lse2 != nullptr) p.lse2[(int64_t)bh * p.M + qrow] = l_tot > 0.f ? lse2 : pos_inf();
+    if (p.lse2 != nullptr) p.lse2[(int64_t)bh * p.M + qpos] = l_tot > 0.f ? lse2 : pos_inf();
     // attention()'s log normalizer m * sm_scale + ln(l) (flash.py:477-483).
     if constexpr (MODE == kFwdPlain)
       if (p.lse_ln != nullptr)
-        p.lse_ln[b * p.sl0 + h * p.sl1 + (int64_t)qrow * p.sl2] =
+        p.lse_ln[b * p.sl0 + qh * p.sl1 + (int64_t)qpos * p.sl2] =
             l_tot > 0.f ? lse2 * 0.69314718055994531f : neg_inf();
   }
   if constexpr (MODE == kFwdRowSum) {
     const float r = xor32_add(rsum);
-    if (g == 0 && qrow < p.M) p.aux[b * p.sa0 + h * p.sa1 + (int64_t)qrow * p.sa2] = r * p.sm_scale;
+    if (g == 0 && row_ok) p.aux[b * p.sa0 + qh * p.sa1 + (int64_t)qpos * p.sa2] = r * p.sm_scale;
   }
 }
 
@@ -781,12 +863,12 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdParams p) {
   }
 }
 
-template <class E, int D, int MODE, int NW, bool DROP>
+template <class E, int D, int MODE, int NW, bool DROP, bool PACK>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdRowSum;
   const int64_t nsplit = kCanSplit ? p.nsplit : 1;
-  const dim3 grid((unsigned)((int64_t)p.nrb * p.B * p.H * nsplit)), block(NW * 64);
-  hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW, DROP>), grid, block, 0, stream, p);
+  const dim3 grid((unsigned)((int64_t)p.nrb * (p.B * p.H / p.pack) * nsplit)), block(NW * 64);
+  hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW, DROP, PACK>), grid, block, 0, stream, p);
   if constexpr (kCanSplit) {
     if (p.nsplit > 1 && p.M > 0) {
       const int64_t nblk = (p.M + 2048 / D - 1) / (2048 / D);
@@ -797,21 +879,21 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int MODE, int NW, bool DROP = false>
+template <int MODE, int NW, bool DROP = false, bool PACK = false>
 hipError_t launch_fwd_mode(const FwdParams& p, int dtype, int d, hipStream_t s) {
   if (dtype == 0) {
     switch (d) {
-      case 16: return launch_fwd_t<F16, 16, MODE, NW, DROP>(p, s);
-      case 32: return launch_fwd_t<F16, 32, MODE, NW, DROP>(p, s);
-      case 64: return launch_fwd_t<F16, 64, MODE, NW, DROP>(p, s);
-      case 128: return launch_fwd_t<F16, 128, MODE, NW, DROP>(p, s);
+      case 16: return launch_fwd_t<F16, 16, MODE, NW, DROP, PACK>(p, s);
+      case 32: return launch_fwd_t<F16, 32, MODE, NW, DROP, PACK>(p, s);
+      case 64: return launch_fwd_t<F16, 64, MODE, NW, DROP, PACK>(p, s);
+      case 128: return launch_fwd_t<F16, 128, MODE, NW, DROP, PACK>(p, s);
     }
   } else {
     switch (d) {
-      case 16: return launch_fwd_t<BF16, 16, MODE, NW, DROP>(p, s);
-      case 32: return launch_fwd_t<BF16, 32, MODE, NW, DROP>(p, s);
-      case 64: return launch_fwd_t<BF16, 64, MODE, NW, DROP>(p, s);
-      case 128: return launch_fwd_t<BF16, 128, MODE, NW, DROP>(p, s);
+      case 16: return launch_fwd_t<BF16, 16, MODE, NW, DROP, PACK>(p, s);
+      case 32: return launch_fwd_t<BF16, 32, MODE, NW, DROP, PACK>(p, s);
+      case 64: return launch_fwd_t<BF16, 64, MODE, NW, DROP, PACK>(p, s);
+      case 128: return launch_fwd_t<BF16, 128, MODE, NW, DROP, PACK>(p, s);
     }
   }
   return hipErrorInvalidValue;

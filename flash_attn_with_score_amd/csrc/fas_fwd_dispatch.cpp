@@ -8,8 +8,17 @@ hipError_t launch_fwd_rowsum(const FwdParams& p, int dtype, int d, hipStream_t s
 hipError_t launch_fwd_scores(const FwdParams& p, int dtype, int d, hipStream_t s);
 hipError_t launch_fwd_region(const FwdParams& p, int dtype, int d, hipStream_t s);
 hipError_t launch_fwd_dropout(const FwdParams& p, int mode, int dtype, int d, hipStream_t s);
+hipError_t launch_fwd_packed(const FwdParams& p, int mode, int dtype, int d, hipStream_t s);
+hipError_t launch_fwd_scores_packed(const FwdParams& p, int dtype, int d, hipStream_t s);
 
+// GQA-packed launches (p.pack > 1) take their own instances; the host never
+// packs a launch with dropout.
 hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, hipStream_t s) {
+  if (p.pack > 1) {
+    if (p.dropout && mode != kFwdRegion) return hipErrorInvalidValue;
+    return mode == kFwdScores ? launch_fwd_scores_packed(p, dtype, d, s)
+                              : launch_fwd_packed(p, mode, dtype, d, s);
+  }
   if (p.dropout && mode != kFwdRegion) return launch_fwd_dropout(p, mode, dtype, d, s);
   switch (mode) {
     case kFwdPlain: return launch_fwd_plain(p, dtype, d, s);

@@ -44,12 +44,18 @@ struct FwdParams {
   int64_t ss0, ss1, ss2;
   int64_t sa0, sa1, sa2;
   int64_t sl0, sl1, sl2;  // lse_ln strides
-  uint32_t q_bytes, k_bytes, v_bytes, o_bytes;  // per-(b, head) buffer extents
+  uint32_t q_bytes, k_bytes, v_bytes, o_bytes;  // buffer extents from (b, first packed head)
   uint32_t qneg;     // 0x80008000 to negate q (negative sm_scale), else 0
   int B, H, G, M, N, split;
   int causal;
   int causal_off;    // key j admissible for query i iff causal_off + i >= j
-  int nrb;           // query row blocks
+  // GQA packing: a workgroup serves `pack` consecutive query heads of one
+  // KV head (pack divides G; 1 = one head per workgroup).  Its rows are
+  // virtual rows v = pos * pack + j (position pos of head h0 + j), so every
+  // K/V tile it stages in LDS is used by all packed heads.
+  int pack;
+  int pack_shift;    // log2(pack) when pack is 1, 2, 4 or 8 (the score writer's packings)
+  int nrb;           // virtual row blocks per group of `pack` heads
   int vec_scores;    // scores rows 16-byte aligned and N % 8 == 0
   int vec_region;    // split % 4 == 0
   int dropout;       // 1: the dropout instances (modes other than kFwdRegion)
@@ -59,7 +65,7 @@ struct FwdParams {
   // (= nrb * rows per workgroup); a combine pass merges them.
   int nsplit;        // 1 = no split
   int tps;
-  int Mpad;
+  int Mpad;          // >= M: row pitch of the partials (positions, not virtual rows)
   float* part_o;     // (B*H, nsplit, Mpad, D) unnormalised O
   float* part_m;     // (B*H, nsplit, Mpad) base-2 exponent offset, -inf if none
   float* part_l;     // (B*H, nsplit, Mpad) sum of the weights

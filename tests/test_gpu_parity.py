@@ -235,3 +235,54 @@ def test_compute_attention_scores(shape, dtype, gpu):
     assert got.dtype == dtype and got.shape == (B, Hq, M, N)
     assert_out_close(got, ref, "scores")
 
+
+
+# GQA packing: a forward workgroup serves all G query heads of its KV head,
+# its rows interleaving the heads (virtual row = position * G + head).
+# Shapes: group sizes 2, 4, 7 and 8; M not a multiple of the block's
+# positions; decode-like M = 1 and M = 3 against long keys (key split);
+# causal M > N (rows with no key); D 16 to 128.  The score writer packs
+# groups of 2, 4 and 8 only (group 7 runs it one head per workgroup).
+PACK_SHAPES = [
+    (1, 8, 2, 100, 300, 64),
+    (2, 8, 1, 1, 700, 128),
+    (1, 14, 2, 3, 2100, 32),
+    (1, 4, 1, 300, 200, 32),
+    (1, 8, 1, 257, 257, 16),
+    (1, 28, 4, 333, 333, 128),
+    # score writer packed over 4 and 8 heads on its 16-byte store path
+    # (N % 8 == 0): M > N, M < N, and a block of positions cut by M
+    (1, 8, 2, 520, 512, 64),
+    (1, 16, 2, 200, 1024, 128),
+    (2, 8, 1, 64, 64, 32),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("shape", PACK_SHAPES, ids=_label)
+@pytest.mark.parametrize("ep", PLAIN_EPS + CROSS_EPS)
+def test_gqa_packed_forward(ep, shape, dtype, gpu):
+    split = max(1, min(shape[3], shape[4]) // 2) if "cross" in ep else None
+    _run(ep, shape, dtype, True, gpu, split=split, seed=17)
+
+
+@pytest.mark.parametrize("ep", PLAIN_EPS)
+def test_gqa_equals_mha_on_repeated_kv(ep, gpu):
+    """The packed GQA launch and the one-head-per-workgroup MHA launch on
+    K/V repeated over the group give the same output and per-query-head side
+    products (column sums of the MHA call folded over each group)."""
+    B, Hq, Hk, M, N, D = 1, 8, 2, 320, 320, 64
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=torch.float16, seed=5, device=gpu)
+    fn = getattr(fas, ep)
+    o1, x1 = fn(q, k, v, causal=True)
+    kr = k.repeat_interleave(Hq // Hk, dim=1).contiguous()
+    vr = v.repeat_interleave(Hq // Hk, dim=1).contiguous()
+    o2, x2 = fn(q, kr, vr, causal=True)
+    torch.cuda.synchronize()
+    assert_out_close(o1, o2.float())
+    if ep == "attention_with_scores":
+        assert_out_close(x1, x2.float(), "scores")
+    elif x1.shape[1] == Hk:
+        assert_sum_close(x1, x2.view(B, Hk, Hq // Hk, -1).sum(2), ep)
+    else:
+        assert_sum_close(x1, x2, ep)
