@@ -4,7 +4,7 @@
 // attention_cross_token_softmax_sum.py:203-268 and the buffered :568-627)
 // are computed after the forward pass, key-block outer: a workgroup owns two
 // blocks of 256 keys of one (batch, query head), keeps them in VGPRs and
-// streams the query rows that can see them.  S = Q K^T puts keys on lanes and
+// streams the query rows that can see them (colsm64_kernel).  S = Q K^T puts keys on lanes and
 // queries in the accumulator registers, so P = exp2(s*qk_scale - lse2[row])
 // (the forward pass's final base-2 log-sum-exp) is summed over queries
 // in-lane.  Every column is owned by one workgroup: no atomics, the result is
@@ -42,39 +42,49 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
   }
 }
 
-// Key blocks of 256 are dealt in mirror pairs (pb, nkb-1-pb): under a causal
-// mask block kb sees (M - 256 kb) query rows, so a pair always sums to the
-// same amount of work and every workgroup finishes together.  The workgroup
-// sweeps block pb, then block nkb-1-pb; each of the 8 waves owns 32 keys of
-// the block and holds their K in VGPRs.  Per 32 x 32 tile a wave issues 8
-// MFMAs (256 cycles) against 16 exp, 16 multiply and 16 add instructions
-// (~300 cycles): the VALU, not the MFMA, bounds this pass.  The row's
+// The column pass with 64 keys per wave.  Each 32x16 Q operand fetched from
+// LDS feeds two MFMAs (the wave's two 32-key sets), so a CU reads half the
+// LDS bytes per MFMA of a wave holding 32 keys (one 1 KiB fetch per
+// v_mfma_32x32x16, which at full MFMA rate on four SIMDs is the whole LDS
+// bandwidth).  Workgroup: 8 waves = 4 key groups (64 keys each, a
+// 256-key block) x 2 row groups; a step stages 128 query rows, row group rg
+// taking rows [64 rg, 64 rg + 64).  The two row groups' column sums of a key
+// are added through LDS at the end of the block, in a fixed order.
+// Key blocks of 256 are dealt in mirror pairs (pb, nkb-1-pb): under a
+// causal mask block kb sees (M - 256 kb) query rows, so a pair always sums
+// to the same amount of work and every workgroup finishes together.  Keys
+// sit on lanes and queries in the accumulator registers; the row's
 // -lse2/qk_scale is the accumulator's starting value, so P = exp2(acc *
-// qk_scale) needs no separate subtraction register.  Holding one block's K
-// at a time (not both blocks', sharing the Q operand) keeps the kernel at
-// ~126 VGPRs; measured 91 -> 85 us at B1 H32 S4096 D128 for both changes.
+// qk_scale) is summed over queries in-lane.  Per 32 x 32 block a wave
+// issues 8 MFMAs against 16 exp, 16 multiply and 16 add instructions, and
+// on this GPU a wave's MFMAs and VALU instructions largely serialise, so
+// the VALU work bounds the pass (measured: 81.8 us with 32 keys per wave,
+// 76.9 us with 64, at B1 H32 S4096 D128 fp16 causal).
 // LN: the row offsets come from a natural-log normalizer (p.lse_ln,
 // total_attention) instead of the forward's base-2 LSE; a template flag so
 // the default copy carries no conversion code in its loop.
 // DROP: the weights pass through the dropout mask before the sum, as the
 // reference's column pass does (attention_with_col_softmax_sum.py:237-244).
+// The sign of a negative sm_scale is applied to K once per block.
 template <class E, int D, bool LN, bool DROP>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(3, 4)))
-void colsm_kernel(const ColsmParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void colsm64_kernel(const ColsmParams p) {
   constexpr int KS = D / 16;
   constexpr int NT = 512;
-  constexpr int BK = 256;           // keys per block (8 waves x 32)
-  constexpr int TQ = 64;            // query rows per tile
+  constexpr int BK = 256;           // keys per block (4 key groups x 64)
+  constexpr int TQ = 128;           // query rows per step (2 row groups x 64)
   constexpr int CPR = D / 8;
   constexpr int CHUNKS = TQ * CPR;
   constexpr int CPT = (CHUNKS + NT - 1) / NT;
 
   __shared__ __attribute__((aligned(16))) uint16_t qlds[2][TQ * D];
   __shared__ __attribute__((aligned(16))) float llds[2][TQ];
+  __shared__ float red[4][64];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
+  const int kg = wave & 3, rg = wave >> 2;
   const int npairs = (p.nkb + 1) / 2;
   int pb, bh;
   map_block_keys(blockIdx.x, npairs, p.B * p.H, pb, bh);
@@ -118,9 +128,7 @@ void colsm_kernel(const ColsmParams p) {
       const int id = tid + i * NT;
       if (CHUNKS % NT == 0 || id < CHUNKS) {
         const int row = id / CPR, ch = id % CPR;
-        // The sign flip is applied here, after the tile's compute, so the
-        // prefetch loads are not waited for at the top of the iteration.
-        *reinterpret_cast<u32x4*>(&qlds[stage][tile_off<D>(row, ch)]) = qst[i] ^ p.qneg;
+        *reinterpret_cast<u32x4*>(&qlds[stage][tile_off<D>(row, ch)]) = qst[i];
       }
     }
     if (tid < TQ) llds[stage][tid] = -lst * inv_scale;
@@ -129,104 +137,110 @@ void colsm_kernel(const ColsmParams p) {
   for (int blk = 0; blk < 2; ++blk) {
     const int kb = blk == 0 ? pb : kbb;
     if (blk == 1 && kbb == pb) break;
-    // Keys of this wave: [key0, key0 + 32).
-    const int key0 = kb * BK + 32 * wave;
-    // K (B operand of S = Q K^T): lane holds K[key0 + c][16ks + 8g, +8).
-    u32x4 kreg[KS];
+    // Keys of this wave: [key0, key0 + 64), set j = keys key0 + 32 j + c.
+    const int key0 = kb * BK + 64 * kg;
+    u32x4 kreg[2][KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      kreg[ks] = buf_load16(rk, (uint32_t)(((key0 + c) * p.sk2 + 16 * ks + 8 * g) * 2));
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        kreg[j][ks] =
+            buf_load16(rk, (uint32_t)(((key0 + 32 * j + c) * p.sk2 + 16 * ks + 8 * g) * 2)) ^ p.qneg;
     // Settle the K loads here: left pending, the compiler's wait counters for
     // them would also hold back (vmcnt N) on the Q prefetch inside the loop.
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[ks]));
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+v"(kreg[j][ks]));
 
-    // Query tiles that can see any key of the block.
+    // Query steps that can see any key of the block.
     int rstart = p.row_lo;
     if (p.causal) rstart = max(rstart, kb * BK - p.causal_off);
     const int t0 = max(0, rstart) / TQ;
 
-    float colacc = 0.f;
+    float colacc[2] = {0.f, 0.f};
     if (t0 < t1) {
       fetch(t0);
       stash(0);
     }
     __syncthreads();
-    // Tile t uses LDS stage (t - t0) & 1, a compile-time constant in each
-    // copy of the step: the per-lane operand addresses are then loop-invariant
-    // and the stage offset folds into the LDS instructions' immediates.
     auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
       constexpr int stage = decltype(stage_tag)::value;
       const bool more = t + 1 < t1;
       if (more) fetch(t + 1);
-      const int r0 = t * TQ;
-      // Live if some row of the tile sees the wave's first key, full if every
-      // row sees its last key.
-      const bool live = !p.causal || p.causal_off + r0 + TQ - 1 >= key0;
-      const bool full = !p.causal || p.causal_off + r0 >= key0 + 31;
-      // Both 32-row query blocks of the tile; the causal mask only where the
-      // wave's keys cross the diagonal (separate code, so full tiles carry no
-      // per-element test).
-      auto body = [&](auto mask_tag) __attribute__((always_inline)) {
-        constexpr bool MASK = decltype(mask_tag)::value;
-        const uint16_t* qt = qlds[stage];
+      const int r0 = t * TQ + 64 * rg;  // this row group's first row
+      const uint16_t* qt = qlds[stage];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < 2; ++qb) {
+        const int rq0 = r0 + 32 * qb;
+        // Live if some row of the block sees the wave's first key, full if
+        // every row sees its last.
+        const bool live = !p.causal || p.causal_off + rq0 + 31 >= key0;
+        const bool full = !p.causal || p.causal_off + rq0 >= key0 + 63;
+        auto body = [&](auto mask_tag) __attribute__((always_inline)) {
+          constexpr bool MASK = decltype(mask_tag)::value;
           // Fenced per query block: the scheduler would otherwise fetch the
-          // next block's operands early and need more than 128 VGPRs.
+          // next block's operands early and run out of registers.
           __builtin_amdgcn_sched_barrier(0);
-          // Operand fetches run two k-steps ahead of their MFMAs (pinned
-          // schedule), so no MFMA waits on a fresh LDS read.
           u32x4 a[KS];
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) a[ks] = lds_row_chunk<D>(qt, 32 * qb + perm_row(c), ks, g);
-          // Register r holds query row r0 + 32qb + acc_row(r, g); it starts at
+          for (int ks = 0; ks < KS; ++ks)
+            a[ks] = lds_row_chunk<D>(qt, 64 * rg + 32 * qb + perm_row(c), ks, g);
+          // Register r holds query row rq0 + acc_row(r, g); it starts at
           // -lse2[row] / qk_scale, so P = exp2(acc * qk_scale).
-          f32x16 s;
+          f32x16 s[2];
 #pragma unroll
           for (int hf = 0; hf < 2; ++hf) {
-            const float* lp = &llds[stage][32 * qb + 16 * hf + 8 * g];
+            const float* lp = &llds[stage][64 * rg + 32 * qb + 16 * hf + 8 * g];
             const f32x4 x0 = *reinterpret_cast<const f32x4*>(lp);
             const f32x4 x1 = *reinterpret_cast<const f32x4*>(lp + 4);
-            s[8 * hf + 0] = x0.x; s[8 * hf + 1] = x0.y; s[8 * hf + 2] = x0.z; s[8 * hf + 3] = x0.w;
-            s[8 * hf + 4] = x1.x; s[8 * hf + 5] = x1.y; s[8 * hf + 6] = x1.z; s[8 * hf + 7] = x1.w;
+            s[0][8 * hf + 0] = x0.x; s[0][8 * hf + 1] = x0.y;
+            s[0][8 * hf + 2] = x0.z; s[0][8 * hf + 3] = x0.w;
+            s[0][8 * hf + 4] = x1.x; s[0][8 * hf + 5] = x1.y;
+            s[0][8 * hf + 6] = x1.z; s[0][8 * hf + 7] = x1.w;
           }
+          s[1] = s[0];
 #pragma unroll
-          for (int ks = 0; ks < KS; ++ks) s = E::mma(a[ks], kreg[ks], s);
+          for (int ks = 0; ks < KS; ++ks) {
+            s[0] = E::mma(a[ks], kreg[0][ks], s[0]);
+            s[1] = E::mma(a[ks], kreg[1][ks], s[1]);
+          }
           {
             constexpr int PD = KS < 2 ? KS : 2;
             __builtin_amdgcn_sched_group_barrier(0x100, PD + 4, 0);  // DS read: 4 of -lse, PD of Q
 #pragma unroll
             for (int i = 0; i < KS; ++i) {
-              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+              __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
               if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
           }
-          // P replaces S in place.
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            s[r] = exp2f_fast(s[r] * p.qk_scale);
-            if constexpr (MASK) {
-              const int row = r0 + 32 * qb + acc_row(r, g);
-              if (p.causal_off + row < key0 + c) s[r] = 0.f;
+          for (int j = 0; j < 2; ++j) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              s[j][r] = exp2f_fast(s[j][r] * p.qk_scale);
+              if constexpr (MASK) {
+                const int row = rq0 + acc_row(r, g);
+                if (p.causal_off + row < key0 + 32 * j + c) s[j][r] = 0.f;
+              }
+              if constexpr (DROP) {
+                const uint32_t row = (uint32_t)(rq0 + acc_row(r, g));
+                const uint32_t idx = ((uint32_t)bh * (uint32_t)p.M + row) * (uint32_t)p.drop.n +
+                                     (uint32_t)(key0 + 32 * j + c);
+                if (!dropout_keep(p.drop, idx)) s[j][r] = 0.f;
+              }
             }
-            if constexpr (DROP) {
-              const uint32_t row = (uint32_t)(r0 + 32 * qb + acc_row(r, g));
-              const uint32_t idx = ((uint32_t)bh * (uint32_t)p.M + row) * (uint32_t)p.drop.n +
-                                   (uint32_t)(key0 + c);
-              if (!dropout_keep(p.drop, idx)) s[r] = 0.f;
-            }
+#pragma unroll
+            for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+              for (int r = 0; r < w; ++r) s[j][r] += s[j][r + w];
+            colacc[j] += s[j][0];
           }
-#pragma unroll
-          for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-            for (int r = 0; r < w; ++r) s[r] += s[r + w];
-          colacc += s[0];
+        };
+        if (live) {
+          if (full) body(std::false_type{});
+          else body(std::true_type{});
         }
-      };
-      if (live) {
-        if (full) body(std::false_type{});
-        else body(std::true_type{});
       }
       if (more) stash(stage ^ 1);
       __syncthreads();
@@ -235,9 +249,24 @@ void colsm_kernel(const ColsmParams p) {
       step(t, std::integral_constant<int, 0>{});
       if (t + 1 < t1) step(t + 1, std::integral_constant<int, 1>{});
     }
-    const float tot = xor32_add(colacc);
-    const int key = key0 + c;
-    if (g == 0 && key < p.ncols) p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot;
+    // Fold the half-waves, then row group 1 into row group 0 (fixed order).
+    float tot[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) tot[j] = xor32_add(colacc[j]);
+    if (rg == 1 && g == 0) {
+      red[kg][c] = tot[0];
+      red[kg][32 + c] = tot[1];
+    }
+    __syncthreads();
+    if (rg == 0 && g == 0) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int key = key0 + 32 * j + c;
+        if (key < p.ncols)
+          p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot[j] + red[kg][32 * j + c];
+      }
+    }
+    __syncthreads();
   }
 }
 
