@@ -248,6 +248,13 @@ void fwd_kernel(const FwdParams p) {
 
   __shared__ __attribute__((aligned(16))) uint16_t kv[2][2][TILE];
   __shared__ __attribute__((aligned(16))) u32x4 stg[SG];
+  // Region tiles (kFwdRegion) leave through LDS too: a wave's 32 x 64 fp32
+  // tile (8 KiB, 16-byte chunks XOR-swizzled by row) is read back row-major,
+  // so each store writes four whole 256-byte row segments; rofs holds each
+  // virtual row's element offset in the region (-1 outside it).
+  constexpr bool kRegion = MODE == kFwdRegion;
+  __shared__ __attribute__((aligned(16))) f32x4 rstg[kRegion ? NW * 512 : 1];
+  __shared__ int64_t rofs[kRegion ? BM : 1];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -528,9 +535,20 @@ void fwd_kernel(const FwdParams p) {
         oacc[db] = E::mma(lds_vt_operand<D>(vt, db, cs, lane), pb[cs], oacc[db]);
   };
 
+  if constexpr (kRegion) {
+    if (tid < BM) {
+      const int v = row0 + tid, pos = v / pack;
+      const int head = h0 + (v - pos * pack);
+      rofs[tid] = pos >= p.split && pos < p.M
+                      ? ((int64_t)(b * p.H + head) * (p.M - p.split) + (pos - p.split)) * p.split
+                      : -1;
+    }
+  }
   if (t_begin < t_end) issue_tile(t_begin, 0);
   if (loader) vm_wait_all();
   lds_barrier();
+  // Whether some row of this wave lies in the region (wave-uniform).
+  const bool wave_region = kRegion && pos_hi(wrow0, 32) >= p.split && pos_lo(wrow0) < p.M;
 
   // The key-tile loop, instantiated once per wave role so that neither copy
   // merges with the other inside the loop.
@@ -611,23 +629,45 @@ void fwd_kernel(const FwdParams p) {
             for (int r = 0; r < 16; ++r) rsum += s[kb][r] == neg_inf() ? 0.f : s[kb][r];
         }
         if constexpr (MODE == kFwdRegion) {
-          if (qpos >= p.split && row_ok && k0 < p.split) {
+          if (p.vec_region) {
+            if (wave_region && k0 < p.split) {
+              // Stage in the MFMA layout: lane (c, g) holds row c, keys
+              // 32 kb + 16 hf + 8 g + (0..7) = chunks 8 kb + 4 hf + 2 g + u.
+              f32x4* tile = &rstg[wave * 512];
+              __builtin_amdgcn_wave_barrier();
+#pragma unroll
+              for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+                  for (int u = 0; u < 2; ++u) {
+                    const int ch = 8 * kb + 4 * hf + 2 * g + u, r0 = 8 * hf + 4 * u;
+                    tile[c * 16 + (ch ^ (c & 15))] =
+                        f32x4{s[kb][r0], s[kb][r0 + 1], s[kb][r0 + 2], s[kb][r0 + 3]};
+                  }
+              __builtin_amdgcn_wave_barrier();
+              // Row-major read-back: lane l takes chunk l % 16 of rows
+              // 4 i + l / 16; keys past split are not stored.
+              const int ch = lane & 15, key = k0 + 4 * ch;
+#pragma unroll
+              for (int i = 0; i < 8; ++i) {
+                const int R = 4 * i + (lane >> 4);
+                const f32x4 val = tile[R * 16 + (ch ^ (R & 15))];
+                const int64_t off = rofs[32 * wave + R];
+                if (off >= 0 && key < p.split)
+                  __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(p.region + off + key));
+              }
+            }
+          } else if (qpos >= p.split && row_ok && k0 < p.split) {
             float* brow = p.region + ((int64_t)bh * (p.M - p.split) + (qpos - p.split)) * p.split;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const f32x16& sv = s[j >> 1];
               const int r0 = 8 * (j & 1);
               const int key0 = k0 + 16 * j + 8 * g;
-              if (p.vec_region && key0 + 8 <= p.split) {
-                *reinterpret_cast<f32x4*>(brow + key0) =
-                    f32x4{sv[r0 + 0], sv[r0 + 1], sv[r0 + 2], sv[r0 + 3]};
-                *reinterpret_cast<f32x4*>(brow + key0 + 4) =
-                    f32x4{sv[r0 + 4], sv[r0 + 5], sv[r0 + 6], sv[r0 + 7]};
-              } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                  if (key0 + e < p.split) brow[key0 + e] = sv[r0 + e];
-              }
+              for (int e = 0; e < 8; ++e)
+                if (key0 + e < p.split) brow[key0 + e] = sv[r0 + e];
             }
           }
         }

@@ -19,8 +19,16 @@ static hipError_t colsm_t(const ColsmParams& p, hipStream_t s) {
 
 hipError_t launch_colsm(const ColsmParams& p, int dtype, int d, bool buffered, hipStream_t s) {
   if (buffered) {
-    const dim3 grid((unsigned)((int64_t)p.nkb * p.B * p.H));
-    hipLaunchKernelGGL(colsm_buffered_kernel, grid, dim3(256), 0, s, p);
+    // 256 keys per workgroup with 16-byte rows, else 64.
+    const bool vec = p.split % 4 == 0;
+    const int64_t nkb = (p.ncols + (vec ? 255 : 63)) / (vec ? 256 : 64);
+    ColsmParams q = p;
+    q.nkb = (int)nkb;
+    const dim3 grid((unsigned)(nkb * p.B * p.H));
+    if (vec)
+      hipLaunchKernelGGL(colsm_buffered_kernel<true>, grid, dim3(256), 0, s, q);
+    else
+      hipLaunchKernelGGL(colsm_buffered_kernel<false>, grid, dim3(256), 0, s, q);
     return hipGetLastError();
   }
   if (dtype == 0) {

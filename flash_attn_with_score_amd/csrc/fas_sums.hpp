@@ -270,35 +270,72 @@ void colsm64_kernel(const ColsmParams p) {
   }
 }
 
-// Buffered source: pass 1 left the raw fp32 scores of the region
-// (rows >= split, keys < split) in p.region; each thread owns one key and
-// walks the rows, so every row read is 1 KiB contiguous per workgroup.
+// Buffered source: pass 1 left the raw fp32 scores of the region (rows >=
+// split, keys < split; masked entries -inf) in p.region.  A workgroup of 4
+// waves owns 256 keys of one (b, h): lane l of every wave holds keys
+// 4 l .. 4 l + 3 and reads them as one 16-byte load per row, so a wave reads
+// 1 KiB contiguous per row; the waves take every fourth row (the row and its
+// lse2 are wave-uniform, the latter a scalar load), several rows in flight,
+// and their sums meet in LDS in a fixed order.  Entries above a key's first
+// admissible row were never written and are excluded by a select.  VEC:
+// split % 4 == 0 (16-byte aligned rows); otherwise one key per lane.
+template <bool VEC>
 __global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p) {
+  constexpr int KPL = VEC ? 4 : 1;  // keys per lane
+  constexpr int BKB = 64 * KPL;     // keys per workgroup
+  __shared__ float red[4][256];
   int kb, bh;
   map_block_keys(blockIdx.x, p.nkb, p.B * p.H, kb, bh);
   const int h = bh % p.H, b = bh / p.H;
-  const int key = kb * 256 + threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int key0 = kb * BKB + KPL * lane;
   const int rows = max(0, p.M - p.split);
-  if (key >= p.ncols) return;
-  const float* reg = p.region + (int64_t)bh * rows * p.split + key;
+  const float* reg = p.region + (int64_t)bh * rows * p.split;
   const float* lse = p.lse2 + (int64_t)bh * p.M;
-  int rstart = p.split;
-  if (p.causal) rstart = max(rstart, key - p.causal_off);
-  float acc = 0.f;
-  int row = rstart;
-  for (; row + 4 <= p.M; row += 4) {
-    float s[4], l[4];
+  // First admissible row of each key, and of the workgroup's first key.
+  int rs[KPL];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      s[u] = reg[(int64_t)(row + u - p.split) * p.split];
-      l[u] = lse[row + u];
+  for (int e = 0; e < KPL; ++e) rs[e] = p.causal ? max(p.split, key0 + e - p.causal_off) : p.split;
+  const int r_lo = p.causal ? max(p.split, kb * BKB - p.causal_off) : p.split;
+  const bool live = key0 < p.ncols;
+  float acc[KPL];
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) acc[e] = 0.f;
+  auto row_step = [&](int row) __attribute__((always_inline)) {
+    const float l = lse[row];
+    const float* rp = reg + (int64_t)(row - p.split) * p.split + key0;
+    float v[KPL];
+    if constexpr (VEC) {
+      const f32x4 x = live ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rp))
+                           : f32x4{0.f, 0.f, 0.f, 0.f};
+      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    } else {
+      v[0] = live ? rp[0] : 0.f;
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc += exp2f_fast(fmaf(s[u], p.qk_scale, -l[u]));
+    for (int e = 0; e < KPL; ++e) {
+      const float w = exp2f_fast(fmaf(v[e], p.qk_scale, -l));
+      acc[e] += row >= rs[e] ? w : 0.f;
+    }
+  };
+  int row = __builtin_amdgcn_readfirstlane(r_lo + wave);
+#pragma unroll 1
+  for (; row + 12 < p.M; row += 16) {
+    row_step(row);
+    row_step(row + 4);
+    row_step(row + 8);
+    row_step(row + 12);
   }
-  for (; row < p.M; ++row)
-    acc += exp2f_fast(fmaf(reg[(int64_t)(row - p.split) * p.split], p.qk_scale, -lse[row]));
-  p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = acc;
+  for (; row < p.M; row += 4) row_step(row);
+#pragma unroll
+  for (int e = 0; e < KPL; ++e) red[wave][KPL * lane + e] = acc[e];
+  __syncthreads();
+  const int t = threadIdx.x;
+  const int key = kb * BKB + t;
+  if (t < BKB && key < p.ncols)
+    p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] =
+        (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
 }
 
 // out[b, hk, j] = sum over the G query heads of group hk of part[b*H + h, j],
