@@ -623,10 +623,24 @@ void fwd_kernel(const FwdParams p) {
           }
         }
         if constexpr (MODE == kFwdRowSum) {
+          // Masked scores (-inf) count as 0; only the masked loop copy can
+          // hold any, so the others add the tile straight (a pairwise tree:
+          // one add per score instead of compare, select and add).
+          float t[16];
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+          for (int r = 0; r < 16; ++r) {
+            float x0 = s[0][r], x1 = s[1][r];
+            if (masked) {
+              x0 = x0 == neg_inf() ? 0.f : x0;
+              x1 = x1 == neg_inf() ? 0.f : x1;
+            }
+            t[r] = x0 + x1;
+          }
 #pragma unroll
-            for (int r = 0; r < 16; ++r) rsum += s[kb][r] == neg_inf() ? 0.f : s[kb][r];
+          for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+            for (int r = 0; r < w; ++r) t[r] += t[r + w];
+          rsum += t[0];
         }
         if constexpr (MODE == kFwdRegion) {
           if (p.vec_region) {
