@@ -126,7 +126,8 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float) -> dict:
+def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float,
+                 scale: float = 1.0) -> dict:
     """Times the CPU oracle (oracle/naive.py, the checker) on whole heads of
     the same workload, cycling over the heads until budget_s of work is
     done; the rate counts the heads actually computed."""
@@ -134,7 +135,7 @@ def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float)
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0)
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0, scale=scale)
     ep = WORKLOADS[name][0]
     side = naive.ENTRY_POINT_OUTPUT[ep]
     offset = naive.ENTRY_POINT_OFFSET[ep]
@@ -183,6 +184,17 @@ def measured_traffic(key):
     except OSError:
         pass
     return None, None
+
+
+def synthetic_qkv(B, Hq, Hk, M, N, D, dtype, scale, device):
+    """q, k, v i.i.d. N(0, 1) * scale, drawn in fp32 from a CPU generator seeded 0
+    (q, then k, then v), rounded to `dtype` and moved to `device`."""
+    g = torch.Generator("cpu").manual_seed(0)
+    out = []
+    for shape in ((B, Hq, M, D), (B, Hk, N, D), (B, Hk, N, D)):
+        out.append((torch.randn(shape, generator=g, dtype=torch.float32) * scale)
+                   .to(dtype).to(device))
+    return tuple(out)
 
 
 def make_call(fas, name, q, k, v, causal, split, dropout_p=0.0):
@@ -262,6 +274,8 @@ def main() -> int:
     ap.add_argument("--non-causal", action="store_true")
     ap.add_argument("--dropout", type=float, default=0.0,
                     help="dropout_p of the forward workloads (default 0, as every config)")
+    ap.add_argument("--input-scale", type=float, default=1.0,
+                    help="q/k/v are N(0,1) times this (BASELINE config 4 uses 0.5)")
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of CPU-oracle work for cpu_baseline (0 disables)")
     ap.add_argument("--no-secondary", action="store_true")
@@ -280,7 +294,6 @@ def main() -> int:
         return 1
 
     import flash_attn_with_score_amd as fas
-    from oracle import inputs
 
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
     B, H, N, D = args.batch, args.heads, args.seqlen, args.head_dim
@@ -299,7 +312,7 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
-    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=0, device=dev)
+    q, k, v = synthetic_qkv(B, H, Hk, M, N, D, dtype, args.input_scale, dev)
     if args.dropout and args.workload == "scores_only":
         print(f"--dropout does not apply to {args.workload}", file=sys.stderr)
         return 2
@@ -338,7 +351,9 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": args.dtype,
-        "data": "synthetic: q/k/v i.i.d. N(0,1) from a seeded CPU generator",
+        "data": "synthetic: q/k/v i.i.d. N(0,1)"
+                + (f" x {args.input_scale:g}" if args.input_scale != 1.0 else "")
+                + " from a seeded CPU generator",
         "config": {"workload": f"{WORKLOADS[args.workload][0]} B{B} H{H}/{Hk} "
                                + (f"S{M}" if M == N else f"M{M} N{N}")
                                + f" D{D} {args.dtype} {'causal' if causal else 'full'}"
@@ -372,7 +387,7 @@ def main() -> int:
     torch.cuda.synchronize()
     if args.cpu_budget > 0 and args.workload not in ("attention_bwd", "scores_only"):
         line["cpu_baseline"] = cpu_baseline(args.workload, B, H, Hk, M, N, D, causal, split,
-                                            dtype, args.cpu_budget)
+                                            dtype, args.cpu_budget, args.input_scale)
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -56,10 +56,12 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
 // sit on lanes and queries in the accumulator registers; the row's
 // -lse2/qk_scale is the accumulator's starting value, so P = exp2(acc *
 // qk_scale) is summed over queries in-lane.  Per 32 x 32 block a wave
-// issues 8 MFMAs against 16 exp, 16 multiply and 16 add instructions, and
-// on this GPU a wave's MFMAs and VALU instructions largely serialise, so
-// the VALU work bounds the pass (measured: 81.8 us with 32 keys per wave,
-// 76.9 us with 64, at B1 H32 S4096 D128 fp16 causal).
+// issues 8 MFMAs against 16 exp, 16 multiply and 16 add instructions
+// (measured: 81.8 us with 32 keys per wave, 76.9 us with 64, at B1 H32
+// S4096 D128 fp16 causal).  Interleaving a block's exponentials with the
+// next block's MFMAs, or streaming Q by LDS DMA in 256-row steps, left the
+// time unchanged: at the board's power limit the energy of this work, not
+// its issue order, bounds the pass.
 // LN: the row offsets come from a natural-log normalizer (p.lse_ln,
 // total_attention) instead of the forward's base-2 LSE; a template flag so
 // the default copy carries no conversion code in its loop.
