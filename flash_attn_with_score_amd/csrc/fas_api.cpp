@@ -646,8 +646,17 @@ static int run_scores(const char* fn, const fas_attn_args* a, const Problem& pr,
   p.B = pr.B; p.H = pr.H; p.G = pr.G; p.M = pr.M; p.N = pr.N;
   p.mask = mask && pr.causal ? 1 : 0;
   p.causal_off = pr.N - pr.M;
-  p.nrb = (pr.M + 255) / 256;
-  p.nkb = (pr.N + 127) / 128;
+  p.nkb = (pr.N + fas::kScoresKeysPerBlock - 1) / fas::kScoresKeysPerBlock;
+  // Row ranges when the key blocks give fewer than 512 workgroups (two per
+  // CU), each at least 4 steps of 64 rows.
+  {
+    const int64_t steps = std::max<int64_t>(1, (pr.M + 63) / 64);
+    const int64_t wgs = (int64_t)pr.B * pr.H * p.nkb;
+    int64_t nrs = wgs >= 512 ? 1 : (512 + wgs - 1) / wgs;
+    nrs = std::max<int64_t>(1, std::min(nrs, steps / 4));
+    p.spr = (int)((steps + nrs - 1) / nrs);
+    p.nrs = (int)((steps + p.spr - 1) / p.spr);
+  }
   p.vec = aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 &&
                   pr.N % 8 == 0
               ? 1

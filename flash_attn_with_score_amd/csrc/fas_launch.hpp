@@ -27,6 +27,8 @@ constexpr int kBwdBlock = 128;
 
 // Scores alone, (q . k) * sm_scale, optionally masked (fas_scores.hpp).
 hipError_t launch_scores(const ScoresParams& p, int dtype, int d, hipStream_t s);
+// Keys per scores-only workgroup (4 key groups x 64 keys).
+constexpr int kScoresKeysPerBlock = 256;
 
 hipError_t launch_fill_zero(float* p, int64_t s0, int64_t s1, int64_t s2, int64_t n0, int64_t n1,
                             int64_t n2, hipStream_t s);

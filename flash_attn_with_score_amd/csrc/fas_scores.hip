@@ -2,14 +2,22 @@
 #include "fas_launch.hpp"
 #include "fas_scores.hpp"
 
+static_assert(fas::kScoresKeysPerBlock == fas::kScoresKeys, "host and kernel key blocks");
+
 namespace fas {
 
 template <class E, int D>
 static hipError_t scores_t(const ScoresParams& p, hipStream_t s) {
-  const int64_t grid = (int64_t)p.B * p.H * p.nrb * p.nkb;
+  const int64_t grid = (int64_t)p.B * p.H * p.nkb * p.nrs;
   if (grid > INT32_MAX) return hipErrorInvalidValue;
-  if (grid > 0)
-    hipLaunchKernelGGL((scores_kernel<E, D>), dim3((unsigned)grid), dim3(64 * kScoresWaves), 0, s, p);
+  if (grid > 0) {
+    if (p.mask)
+      hipLaunchKernelGGL((scores_kernel<E, D, true>), dim3((unsigned)grid), dim3(64 * kScoresWaves),
+                         0, s, p);
+    else
+      hipLaunchKernelGGL((scores_kernel<E, D, false>), dim3((unsigned)grid), dim3(64 * kScoresWaves),
+                         0, s, p);
+  }
   return hipGetLastError();
 }
 

@@ -5,145 +5,201 @@
 // the score output of attention_with_scores for short query ranges, where
 // the fused score writer would run one workgroup per head (masked entries
 // written as 0, attention_with_scores.py:141-148).  The work is a write
-// stream, so the stores are shaped for HBM: every score leaves in a whole
-// 128-byte run of one row.
+// stream, so the kernel is shaped by what the HBM takes best (store-only
+// probes on the MI355X, 1 GiB of 8 KiB rows): every store instruction writes
+// whole 128-byte row runs (partial rows run at a sixth of the rate), and few
+// rows are written at once over the chip, each in long runs (256 rows per
+// workgroup advancing 128 bytes at a time: 3.5 TB/s; 32 rows per workgroup
+// written by four concurrent streams: 5.9 TB/s).
 //
-// A workgroup of four waves takes 256 query rows and 128 keys.  The keys' K
-// rows are copied once into a swizzled LDS tile.  Each wave holds 64 query
-// rows of Q (two 32-row B operands of S^T = K Q^T) and runs over the tile in
-// 64-key chunks: two 32-key A operands from LDS, four MFMA blocks.  Lane
-// (c, g) then owns rows c and 32 + c and keys 16*hf + 8g + [0, 8) of each
-// block; the wave packs its 64 x 64 chunk into a private LDS stage (16-byte
-// units XOR-swizzled by row) and reads it back row-major, eight lanes per
-// 128-byte row run, for non-temporal 16-byte stores.
+// A workgroup owns 256 keys of one head and walks all query rows in steps
+// of 64.  Its 8 waves are 4 key groups (64 keys, held in VGPRs for the
+// workgroup's life as the A operands of S^T = K Q^T) x 2 row groups (32 rows
+// of the step).  Each step's 64 Q rows pass through LDS (double-buffered,
+// loaded through registers, so the compiler's wait counts cover them beside
+// the score stores); every wave turns its 32 x 64 score tile into 16-bit
+// values in a private LDS stage that it reads back row-major: four
+// non-temporal stores of 8 rows x 128 bytes.  The key blocks of a head run
+// side by side on one XCD (its L2 holds the head's Q once), advance through
+// the rows at the same pace, and so write each score row as several
+// concurrent 512-byte runs while only a few thousand rows are open over the
+// chip.  Q is read once per key block, K once.
 #pragma once
 #include "fas_device.hpp"
 #include "fas_params.hpp"
 
 namespace fas {
 
-constexpr int kScoresWaves = 4;
-constexpr int kScoresRows = 64 * kScoresWaves;  // query rows per workgroup
-constexpr int kScoresKeys = 128;                // keys per workgroup, staged in LDS
+// Byte offset past every buffer extent: the store is dropped.
+constexpr uint32_t kOffNoneScores = 0x80000000u;
 
-template <class E, int D>
-__global__ __launch_bounds__(64 * kScoresWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void scores_kernel(const ScoresParams p) {
+constexpr int kScoresWaves = 8;
+constexpr int kScoresRows = 64;    // query rows per step (2 row groups x 32)
+constexpr int kScoresKeys = 256;   // keys per workgroup (4 key groups x 64)
+
+// MASK: the causal / key-range mask of attention_with_scores (entries with
+// key > causal_off + row written as 0); a template flag, so the unmasked
+// instance (compute_attention_scores) carries no per-score compare.
+template <class E, int D, bool MASK>
+__global__ __launch_bounds__(64 * kScoresWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void scores_kernel(const ScoresParams p) {
   constexpr int KS = D / 16;
-  __shared__ __attribute__((aligned(16))) uint16_t ktile[kScoresKeys * D];
-  __shared__ __attribute__((aligned(16))) uint16_t stage_all[kScoresWaves][64 * 64];
+  constexpr int CPR = D / 8;                                   // 16-byte chunks per row
+  constexpr int QCH = kScoresRows * CPR;                       // chunks of a step's Q rows
+  constexpr int CPT = (QCH + 64 * kScoresWaves - 1) / (64 * kScoresWaves);
+  __shared__ __attribute__((aligned(16))) uint16_t qtile[2][kScoresRows * D];
+  __shared__ __attribute__((aligned(16))) u32x4 stg[kScoresWaves][256];
+
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
-  const int kblk = blockIdx.x % p.nkb;
-  const int rest = blockIdx.x / p.nkb;
-  const int rb = rest % p.nrb, bh = rest / p.nrb;
+  const int kg = wave & 3, rg = wave >> 2;
+  // A head has nkb key blocks x nrs row ranges (row ranges only when the key
+  // blocks alone leave the chip short of workgroups).  Workgroups go to the
+  // 8 XCDs round-robin by id.  With B*H a multiple of 8 each XCD takes a
+  // contiguous set of heads, so a head's workgroups run together on one XCD.
+  int kb, rs, bh;
+  {
+    const int bid = blockIdx.x, heads = p.B * p.H, per_head = p.nkb * p.nrs;
+    int w;
+    if ((heads & 7) == 0) {
+      const int per = heads >> 3, x = bid & 7, sidx = bid >> 3;
+      bh = x * per + sidx / per_head;
+      w = sidx % per_head;
+    } else {
+      bh = bid / per_head;
+      w = bid % per_head;
+    }
+    rs = w / p.nkb;
+    kb = w % p.nkb;
+  }
   const int b = bh / p.H, h = bh % p.H, hk = h / p.G;
-  const int key_base = kScoresKeys * kblk;
-  const int row0 = kScoresRows * rb + 64 * wave;  // the wave's first row
-  uint16_t* stage = stage_all[wave];
-  // Key j is kept for row i iff j <= causal_off + i.  A workgroup whose keys
-  // all lie above its last row's diagonal only writes zeros.
-  const bool live = !p.mask || key_base <= p.causal_off + kScoresRows * (rb + 1) - 1;
-  if (live)
-    dma_tile<D, kScoresKeys, kScoresWaves>(
-        make_rsrc_words(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes), p.sk2, key_base,
-        lds_addr(ktile), wave, lane);
-  u32x4 qreg[2][KS];
-  if (row0 < p.M) {
-    const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        qreg[hh][ks] =
-            buf_load16(rq, (uint32_t)(((row0 + 32 * hh + c) * p.sq2 + 16 * ks + 8 * g) * 2));
-  }
-  if (live) {
-    vm_wait_all();
-    __builtin_amdgcn_s_barrier();
-  }
-  if (row0 >= p.M) return;
+  const int k0 = kScoresKeys * kb + 64 * kg;  // the wave's first key
+  // This workgroup's steps of 64 rows: [t_begin, t_end).
+  const int nsteps = (p.M + kScoresRows - 1) / kScoresRows;
+  const int t_begin = min(nsteps, rs * p.spr), t_end = min(nsteps, t_begin + p.spr);
 
-  uint16_t* sbase = p.scores + b * p.ss0 + h * p.ss1;
-  for (int ch = 0; ch < kScoresKeys / 64; ++ch) {
-    const int kc = key_base + 64 * ch;
-    if (kc >= p.N) break;
-    f32x16 s[2][2];  // [row half][32-key block]
+  // The wave's 64 keys as A operands (keys past N read as zeros).
+  u32x4 a0[KS], a1[KS];
+  {
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int key0 = kc + 32 * kb;
-      s[0][kb] = f32x16{};
-      s[1][kb] = f32x16{};
-      // Blocks above the wave's diagonal skip the MFMAs (all entries masked).
-      if (live && key0 < p.N && (!p.mask || key0 <= p.causal_off + row0 + 63)) {
+    for (int ks = 0; ks < KS; ++ks) {
+      a0[ks] = buf_load16(rk, (uint32_t)(((k0 + perm_row(c)) * p.sk2 + 16 * ks + 8 * g) * 2));
+      a1[ks] = buf_load16(rk, (uint32_t)(((k0 + 32 + perm_row(c)) * p.sk2 + 16 * ks + 8 * g) * 2));
+    }
+  }
+  // Q rows of step t: chunk tid + 512 i is (row, 16-byte chunk ch); rows
+  // past M read as zeros.
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
+  u32x4 qst[CPT];
+  auto load_q = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const u32x4 a = lds_row_chunk<D>(ktile, 64 * ch + 32 * kb + perm_row(c), ks, g);
-          s[0][kb] = E::mma(a, qreg[0][ks], s[0][kb]);
-          s[1][kb] = E::mma(a, qreg[1][ks], s[1][kb]);
-        }
+    for (int i = 0; i < CPT; ++i) {
+      const int id = tid + 64 * kScoresWaves * i;
+      if (QCH % (64 * kScoresWaves) == 0 || id < QCH) {
+        const int row = t * kScoresRows + id / CPR, ch = id % CPR;
+        qst[i] = buf_load16(rq, (uint32_t)((row * p.sq2 + ch * 8) * 2));
       }
     }
-    // Register r of block kb holds key kc + 32kb + 16*(r/8) + 8g + r%8.
-    if (p.vec) {
-      // The wave's private stage is written in the MFMA layout and read back
-      // row-major by other lanes of the same wave.  A wave's LDS accesses
-      // execute in issue order, so a wave barrier (no instruction, an
-      // ordering point for the compiler) on each side of the hand-over is
-      // all the synchronisation this needs: before the read-back, and before
-      // the next chunk overwrites the stage.
-      __builtin_amdgcn_wave_barrier();
+  };
+  auto write_q = [&](int stage) __attribute__((always_inline)) {
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int r = 32 * hh + c, row = row0 + r;
+    for (int i = 0; i < CPT; ++i) {
+      const int id = tid + 64 * kScoresWaves * i;
+      if (QCH % (64 * kScoresWaves) == 0 || id < QCH)
+        *reinterpret_cast<u32x4*>(&qtile[stage][tile_off<D>(id / CPR, id % CPR)]) = qst[i];
+    }
+  };
+
+  uint16_t* const shead = p.scores + b * p.ss0 + h * p.ss1;
+  const bool key_ok = k0 + 8 * (lane & 7) < p.N;  // the lane's store unit lies below N
+  if (t_begin < t_end) {
+    load_q(t_begin);
+    write_q(0);
+  }
+  lds_barrier();
+  u32x4* const st = stg[wave];
+  for (int t = t_begin; t < t_end; ++t) {
+    const int stage = (t - t_begin) & 1;
+    if (t + 1 < t_end) load_q(t + 1);
+    const int row0 = t * kScoresRows;      // the step's first row
+    const int wrow0 = row0 + 32 * rg;      // the wave's first row
+    // S^T tile: register r of s[j] holds key k0 + 32j + 16(r/8) + 8g + r%8
+    // of query row wrow0 + c.  Every tile runs its MFMAs: keys past N hold
+    // zero K rows, and masked entries are zeroed below (a branch around the
+    // MFMAs would cost 32 register moves per tile to merge the zeros).
+    f32x16 s[2];
+    {
+      const uint16_t* qt = qtile[stage];
+      u32x4 qb[KS];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int ks = 0; ks < KS; ++ks) qb[ks] = lds_row_chunk<D>(qt, 32 * rg + c, ks, g);
+      s[0] = E::mma(a0[0], qb[0], f32x16{});
+      s[1] = E::mma(a1[0], qb[0], f32x16{});
 #pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            const int u = 4 * kb + 2 * hf + g;  // 16-byte unit of the 64-key row run
-            const int k8 = kc + 8 * u;
-            float v[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              v[e] = s[hh][kb][8 * hf + e] * p.sm_scale;
-              if (p.mask && p.causal_off + row < k8 + e) v[e] = 0.f;
-            }
-            *reinterpret_cast<u32x4*>(stage + r * 64 + ((u ^ (r & 7)) << 3)) =
-                u32x4{E::pack(v[0], v[1]), E::pack(v[2], v[3]), E::pack(v[4], v[5]),
-                      E::pack(v[6], v[7])};
-          }
+      for (int ks = 1; ks < KS; ++ks) {
+        s[0] = E::mma(a0[ks], qb[ks], s[0]);
+        s[1] = E::mma(a1[ks], qb[ks], s[1]);
       }
+    }
+    const int row = wrow0 + c;  // the lane's query row
+    if (p.vec) {
+      // Stage row c, 16-byte unit u = 4j + 2hf + g at c*8 + (u ^ ((c/2) & 7)):
+      // conflict-free for these writes (one unit of 32 rows) and for the
+      // row-major reads below (8 units of 8 rows).  The stage is private to
+      // the wave and LDS accesses of a wave execute in order, so wave
+      // barriers (compiler ordering points) suffice around the hand-over.
       __builtin_amdgcn_wave_barrier();
-      // Row-major read-back: lane l takes unit l % 8 of rows l / 8 + 8i.
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int u = 4 * j + 2 * hf + g;
+          float v[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            v[e] = s[j][8 * hf + e] * p.sm_scale;
+            if (MASK && p.causal_off + row < k0 + 8 * u + e) v[e] = 0.f;
+          }
+          st[c * 8 + (u ^ ((c >> 1) & 7))] =
+              u32x4{E::pack(v[0], v[1]), E::pack(v[2], v[3]), E::pack(v[4], v[5]),
+                    E::pack(v[6], v[7])};
+        }
+      __builtin_amdgcn_wave_barrier();
+      // Lane l stores unit l % 8 of rows l / 8 + 8i: whole 128-byte runs.
+      // The buffer ends at the wave's last key below N in its last row below
+      // M (row stride >= N), so stores to rows past M drop out.
+      const int nrows = min(32, p.M - wrow0), nkeys = min(64, p.N - k0);
+      const __amdgpu_buffer_rsrc_t rs =
+          make_rsrc(shead + (int64_t)wrow0 * p.ss2 + k0,
+                    __builtin_amdgcn_readfirstlane(
+                        nrows > 0 && nkeys > 0
+                            ? (uint32_t)(((int64_t)(nrows - 1) * p.ss2 + nkeys) * 2)
+                            : 0u));
       const int u = lane & 7;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int r = (lane >> 3) + 8 * i, row = row0 + r;
-        const u32x4 val = *reinterpret_cast<const u32x4*>(stage + r * 64 + ((u ^ (r & 7)) << 3));
-        if (row < p.M && kc + 8 * u < p.N)
-          __builtin_nontemporal_store(
-              val, reinterpret_cast<u32x4*>(sbase + (int64_t)row * p.ss2 + kc + 8 * u));
+      for (int i = 0; i < 4; ++i) {
+        const int r = (lane >> 3) + 8 * i;
+        const u32x4 val = st[r * 8 + (u ^ ((r >> 1) & 7))];
+        buf_store16_nt(val, rs, key_ok ? (uint32_t)((r * p.ss2 + 8 * u) * 2) : kOffNoneScores);
       }
-    } else {
+    } else if (row < p.M) {
+      uint16_t* sr = shead + (int64_t)row * p.ss2;
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int row = row0 + 32 * hh + c;
-        if (row >= p.M) continue;
-        uint16_t* srow = sbase + (int64_t)row * p.ss2;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-          for (int hf = 0; hf < 2; ++hf) {
-            const int k8 = kc + 32 * kb + 16 * hf + 8 * g;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              float v = s[hh][kb][8 * hf + e] * p.sm_scale;
-              if (p.mask && p.causal_off + row < k8 + e) v = 0.f;
-              if (k8 + e < p.N) srow[k8 + e] = E::cvt(v);
-            }
+          for (int e = 0; e < 8; ++e) {
+            const int key = k0 + 32 * j + 16 * hf + 8 * g + e;
+            float v = s[j][8 * hf + e] * p.sm_scale;
+            if (MASK && p.causal_off + row < key) v = 0.f;
+            if (key < p.N) sr[key] = E::cvt(v);
           }
-      }
     }
+    if (t + 1 < t_end) write_q(stage ^ 1);
+    lds_barrier();
   }
 }
 

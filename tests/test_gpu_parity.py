@@ -218,7 +218,10 @@ def test_repeat_calls_bit_identical(ep, shape, gpu):
 
 @pytest.mark.parametrize("shape", [(1, 4, 2, 96, 200, 64), (2, 2, 1, 33, 1000, 128),
                                    (1, 3, 3, 300, 70, 16), (1, 2, 2, 64, 64, 32),
-                                   (1, 2, 2, 600, 520, 128), (1, 2, 1, 513, 1029, 64)],
+                                   (1, 2, 2, 600, 520, 128), (1, 2, 1, 513, 1029, 64),
+                                   # fewer keys than one 64-key group, rows past M in
+                                   # the last step (16-byte and element-wise stores)
+                                   (1, 2, 2, 100, 40, 32), (2, 1, 1, 70, 8, 16)],
                          ids=_label)
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 def test_compute_attention_scores(shape, dtype, gpu):
