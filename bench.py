@@ -168,6 +168,7 @@ def cpu_baseline(name, B, H, Hk, M, N, D, causal, split, dtype, budget_s: float,
 # produced it.
 TRAFFIC_SUMMARIES = {
     ("scores", 1, 32, 32, 4096, 128, "fp16", True): "attn_fwd_scores_f16_b1h32s4096d128_causal.md",
+    ("scores_only", 1, 32, 32, 4096, 128, "fp16", True): "scores_only_f16_b1h32s4096d128.md",
 }
 
 
