@@ -193,8 +193,12 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
       if (more) fetch(t + 1, stage ^ 1);
       const uint16_t* qt = qlds[stage];
       const uint16_t* gt = glds[stage];
-      auto body = [&](int qb, auto mask_tag) __attribute__((always_inline)) {
-        constexpr bool MASK = decltype(mask_tag)::value;
+      // One 32-row block.  The mask (diagonal blocks only) changes the
+      // weights alone: the masked and unmasked copies of the elementwise
+      // part join before the dV / dK products, so the 128 accumulator
+      // registers stay on one code path (two copies of the whole block gave
+      // them different registers, merged by 128 moves per block).
+      auto body = [&](int qb, bool full) __attribute__((always_inline)) {
         const int r0 = t * TQ + 32 * qb;
         // Register r holds query row r0 + acc_row(r, g) and key key0 + c.
         f32x16 s = f32x16{}, dp;
@@ -213,23 +217,29 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
         f32x16 nl;
         load8(nl, &nlds[stage][32 * qb + 8 * g], 0, 0);
         load8(nl, &nlds[stage][32 * qb + 16 + 8 * g], 0, 1);
+        f32x16 pr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pr[r] = exp2f_fast(fmaf(s[r], qk, nl[r]));
+        if (!full) {
+          // Row r0 + acc_row(r, g) sees key key0 + c iff acc_row(r, g) >= lim.
+          const int lim = key0 + c - p.causal_off - r0;
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (acc_row(r, g) < lim) pr[r] = 0.f;
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float pr = exp2f_fast(fmaf(s[r], qk, nl[r]));
-          if constexpr (MASK) {
-            if (p.causal_off + r0 + acc_row(r, g) < key0 + c) pr = 0.f;
-          }
           if constexpr (DROP) {
             const uint32_t idx =
                 ((uint32_t)bh * (uint32_t)p.M + (uint32_t)(r0 + acc_row(r, g))) *
                     (uint32_t)p.N + (uint32_t)(key0 + c);
             const bool keep = dropout_keep(p.drop, idx);
             const float nd = xlds[stage][32 * qb + acc_row(r, g)];  // -delta
-            s[r] = keep ? pr : 0.f;
-            dp[r] = pr * ((keep ? p.drop.scale * dp[r] : 0.f) + nd);
+            s[r] = keep ? pr[r] : 0.f;
+            dp[r] = pr[r] * ((keep ? p.drop.scale * dp[r] : 0.f) + nd);
           } else {
-            s[r] = pr;
-            dp[r] = pr * dp[r];
+            s[r] = pr[r];
+            dp[r] = pr[r] * dp[r];
           }
         }
         const u32x4 pb0 = pack_b<E>(s, 0), pb1 = pack_b<E>(s, 1);
@@ -252,10 +262,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
         // first row sees the wave's last key.
         const bool live = !p.causal || p.causal_off + r0 + 31 >= key0;
         const bool full = !p.causal || p.causal_off + r0 >= key0 + 31;
-        if (live) {
-          if (full) body(qb, std::false_type{});
-          else body(qb, std::true_type{});
-        }
+        if (live) body(qb, full);
       }
       if (more) {
         vm_wait_all();
