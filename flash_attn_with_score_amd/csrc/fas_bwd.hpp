@@ -429,8 +429,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     if (more) fetch(t + 1, stage ^ 1);
     const uint16_t* kt = klds[stage];
     const uint16_t* vt = vlds[stage];
-    auto body = [&](int kb2, auto mask_tag) __attribute__((always_inline)) {
-      constexpr bool MASK = decltype(mask_tag)::value;
+    // One 32-key sub-block.  The mask (tiles at the diagonal or the key
+    // edge) only zeroes weights, and both cases join before the dQ
+    // products, so the dQ accumulators stay on one code path.
+    auto body = [&](int kb2, bool full) __attribute__((always_inline)) {
       const int kbase = t * BN + 32 * kb2;
       // Fenced per sub-block, operand fetches pinned two k-steps ahead of
       // their MFMAs: left free, the scheduler hoists every fetch of the tile
@@ -444,12 +446,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         ak[ks] = lds_row_chunk(kt + 32 * kb2 * D, ro, ks);
         av[ks] = lds_row_chunk(vt + 32 * kb2 * D, ro, ks);
       }
-      // Register r holds key kbase + acc_row(r, g) for query row qrow.
-      f32x16 s = f32x16{}, dp;
+      // Register r holds key kbase + acc_row(r, g) for query row qrow.  S
+      // starts from a zero accumulator (an inline constant of the first
+      // MFMA), dP - delta from -delta.
+      f32x16 s, dp;
 #pragma unroll
       for (int r = 0; r < 16; ++r) dp[r] = DROP ? 0.f : xl;
+      s = E::mma(ak[0], qreg[0], f32x16{});
+      dp = E::mma(av[0], greg[0], dp);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
+      for (int ks = 1; ks < KS; ++ks) {
         s = E::mma(ak[ks], qreg[ks], s);
         dp = E::mma(av[ks], greg[ks], dp);
       }
@@ -462,13 +468,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
         }
       }
+      // Key kbase + acc_row(r, g) is admissible iff acc_row(r, g) < lim.
+      const int lim = (p.causal ? min(p.N, p.causal_off + qrow + 1) : p.N) - kbase;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         float pr = exp2f_fast(fmaf(s[r], qk, nl));
-        if constexpr (MASK) {
-          const int key = kbase + acc_row(r, g);
-          if (key >= p.N || (p.causal && p.causal_off + qrow < key)) pr = 0.f;
-        }
+        if (!full && acc_row(r, g) >= lim) pr = 0.f;
         if constexpr (DROP) {
           const uint32_t idx = drow + (uint32_t)(kbase + acc_row(r, g));
           dp[r] = pr * ((dropout_keep(p.drop, idx) ? p.drop.scale * dp[r] : 0.f) + xl);
@@ -499,10 +504,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int kb2 = 0; kb2 < 2; ++kb2) {
         // Sub-blocks past this wave's last visible key are skipped.
-        if (t * BN + 32 * kb2 < whi) {
-          if (t < tfull) body(kb2, std::false_type{});
-          else body(kb2, std::true_type{});
-        }
+        if (t * BN + 32 * kb2 < whi) body(kb2, t < tfull);
       }
     }
     if (more) vm_wait_all();
