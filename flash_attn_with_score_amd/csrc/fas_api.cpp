@@ -15,6 +15,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
+#include <vector>
 #include <string>
 
 #include "fas_launch.hpp"
@@ -59,6 +60,25 @@ int check_tensor(const char* fn, const char* name, const void* ptr, const int64_
   if ((rows + 512) * st[2] * 2 >= kMaxSliceBytes)
     return fail(FAS_ERR_UNSUPPORTED, fn, "%s (batch, head) slice exceeds 2 GiB", name);
   return FAS_OK;
+}
+
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+int device_cu_count() {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if ((size_t)dev >= cache.size()) cache.resize((size_t)dev + 1, 0);
+  if (cache[(size_t)dev] == 0) {
+    int n = 0;
+    cache[(size_t)dev] =
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+            ? n
+            : 256;
+  }
+  return cache[(size_t)dev];
 }
 
 uint32_t slice_bytes(int64_t rows, int64_t row_stride, int64_t D) {
@@ -218,6 +238,7 @@ fas::FwdParams fwd_params(const fas_attn_args* a, const Problem& pr, bool top_le
   p.pack = pr.pack;
   p.pack_shift = pr.pack == 1 ? 0 : pr.pack == 2 ? 1 : pr.pack == 4 ? 2 : pr.pack == 8 ? 3 : -1;
   p.nrb = (int)(((int64_t)pr.M * pr.pack + rows_per_block - 1) / rows_per_block);
+  p.bm = rows_per_block;
   p.nsplit = 1;
   p.sm_scale = std::fabs(pr.sm_scale);
   p.qk_scale = qk_scale_of(pr.sm_scale);
@@ -685,7 +706,7 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
     if ((rc = run_fwd(fn, p, pr, fas::kFwdPlain, stream))) return rc;
     return run_scores(fn, a, pr, scores, st, true, stream);
   }
-  const int bm = fas::kFwdRows;
+  int bm = fas::kFwdRows;
   // The score writer packs 2, 4 or 8 heads (its store layout keeps a lane's
   // head fixed) and addresses their score rows from the first head's, below
   // offset 2^31; otherwise each workgroup takes one head.
@@ -694,6 +715,14 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
       ((pw.pack != 2 && pw.pack != 4 && pw.pack != 8) ||
        ((int64_t)(pw.pack - 1) * st[1] + (int64_t)(bm / pw.pack + 2) * st[2]) * 2 >= kMaxSliceBytes))
     pw.pack = 1;
+  // One workgroup runs per CU.  When 256-row blocks would all run in one
+  // round (the longest causal row block is then the critical path), unpacked
+  // launches take 128-row blocks (4 waves): twice the workgroups, in two
+  // rounds the mirror order balances (B1 H32 S1024: 45.7 -> 37.5 us; H16
+  // S4096: 179 -> 145 us; H32 S2048: 94.3 -> 95.9 us).
+  if (pw.pack == 1 &&
+      (int64_t)pr.B * pr.H * ((pr.M + fas::kFwdRows - 1) / fas::kFwdRows) <= device_cu_count())
+    bm = fas::kFwdRows / 2;
   fas::FwdParams p = fwd_params(a, pw, false, bm);
   rescale_dropout(p, a);
   p.scores = static_cast<uint16_t*>(scores);
@@ -702,6 +731,9 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
   p.ss2 = st[2];
   p.vec_scores =
       aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && pr.N % 8 == 0;
+  // The writer runs one workgroup per CU; with no more workgroups than CUs
+  // they all run at once and each writes its own zero triangle.
+  p.zero_self = (int64_t)p.nrb * (pr.B * pr.H / pw.pack) <= device_cu_count() ? 1 : 0;
   return run_fwd(fn, p, pr, fas::kFwdScores, stream);
 }
 

@@ -33,9 +33,11 @@
 //    softmax (every term is divided by the same l at the end).
 //  * Masks are applied only on tiles that cross the causal diagonal or the
 //    key-length edge; all other tiles take an unmasked path.
-//  * Score writer (kFwdScores, 8 waves): waves 0-3 ("loaders") fetch K/V
-//    and never store inside the loop, so their wait for the DMA is never a
-//    wait for stores; waves 4-7 ("storers") issue every global score store.
+//  * Score writer (kFwdScores, 8 waves, or 4 with 128-row blocks when 256-row
+//    blocks would leave CUs idle): the first half of the waves ("loaders")
+//    fetch K/V and never store inside the loop, so their wait for the DMA is
+//    never a wait for stores; the second half ("storers") issue every global
+//    score store.
 //    A CU can only drain stores at its share of HBM write bandwidth, and a
 //    wave that issues a store into a full queue stalls, so each storer
 //    spreads a fixed number of stores per key tile between its MFMAs
@@ -47,7 +49,8 @@
 //    (measured 355 -> 316 us at B1 H32 S4096 D128).
 //    Each workgroup writes the zeros of its *mirror* row block nrb-1-rb, so
 //    long-running workgroups carry the zeros of short ones and the write
-//    stream stays even over the kernel's life.
+//    stream stays even over the kernel's life -- unless every workgroup runs
+//    at once (p.zero_self), where each writes its own.
 #pragma once
 #include "fas_device.hpp"
 #include "fas_params.hpp"
@@ -225,7 +228,8 @@ __device__ __forceinline__ void sched_score_tile() {
 template <class E, int D, int MODE, int NW, bool DROP, bool PACK>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void fwd_kernel(const FwdParams p) {
-  static_assert(MODE != kFwdScores || NW == 8, "the score writer uses 8 waves");
+  static_assert(MODE != kFwdScores || NW == 8 || NW == 4, "the score writer uses 4 or 8 waves");
+  constexpr int NH = NW / 2;  // score writer: loader waves [0, NH), storer waves [NH, NW)
   const int pack = PACK ? p.pack : 1;
   constexpr int KS = D / 16;               // MFMA k-steps over the head dim
   constexpr int DB = (D + 31) / 32;        // 32-dim blocks of O^T
@@ -236,13 +240,13 @@ void fwd_kernel(const FwdParams p) {
   constexpr int RPB = 512 / D;             // tile rows per DMA block
   constexpr int CPR = D / 8;               // 16-byte chunks per row
   constexpr bool kSplit = MODE == kFwdScores;
-  constexpr int NL = kSplit ? 4 : NW;      // waves issuing tile loads
+  constexpr int NL = kSplit ? NH : NW;     // waves issuing tile loads
   constexpr int QPW = (BLOCKS + NL - 1) / NL;
   // Score tiles leave through LDS (4 KiB per 32-row wave tile), so that
   // every global store instruction writes 8 full 128-byte row segments:
-  // 2 stages x 4 loader tiles, then one tile per storer.
+  // 2 stages x NH loader tiles, then one tile per storer.
   constexpr int TSZ = 256;  // 16-byte units per wave tile
-  constexpr int SG = kSplit ? (8 + 4) * TSZ : 1;
+  constexpr int SG = kSplit ? 3 * NH * TSZ : 1;
   // Zero-store slots per key tile and storer (issued during O += P V).
   constexpr int kZero = 8;  // zero stores per key tile: one ZeroRuns batch
 
@@ -259,7 +263,7 @@ void fwd_kernel(const FwdParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
-  const bool loader = !kSplit || wave < 4;
+  const bool loader = !kSplit || wave < NH;
 
   // Split over keys: the plain and row-sum modes may give a row block to
   // nsplit workgroups, each over its own share of the key tiles.
@@ -354,7 +358,7 @@ void fwd_kernel(const FwdParams p) {
   // writes its own scores element-wise.
   const bool vec = MODE == kFwdScores && p.vec_scores != 0;
   const bool storer = vec && !loader;
-  const int pwave = wave - 4;  // the loader wave a storer serves
+  const int pwave = wave - NH;  // the loader wave a storer serves
   const int pwtiles = kSplit ? wtiles_of(row0 + 32 * pwave) : 0;
   // Lane (row l/8, chunk l%8) of an 8-row x 128-byte store.
   const int lane_key = 8 * (lane & 7);
@@ -379,8 +383,10 @@ void fwd_kernel(const FwdParams p) {
                    __builtin_amdgcn_readfirstlane(hspan + (uint32_t)((pos1 - pos0) * p.ss2 * 2)));
     gs = RowGeom{sshift, p.M, pos0, (uint32_t)(p.ss2 * 2), (uint32_t)(p.ss1 * 2)};
     lane_off = gs.lane_off(lane);
-    // Zeros of the mirror row block.
-    const int mrow0 = (p.nrb - 1 - rb) * BM;
+    // Zeros of the mirror row block, or of its own when every workgroup
+    // runs at once (then the longest row blocks would also carry the largest
+    // triangles).
+    const int mrow0 = (p.zero_self ? rb : p.nrb - 1 - rb) * BM;
     const int mpos0 = min(p.M, pos_lo(mrow0));
     const int mpos1 = min(p.M, pos_lo(mrow0 + BM - 1) + 1);
     rz = make_rsrc(p.scores + b * p.ss0 + h0 * p.ss1 + (int64_t)mpos0 * p.ss2,
@@ -448,8 +454,8 @@ void fwd_kernel(const FwdParams p) {
   auto staged_pair = [&](int t, u32x4 (&w)[8], uint32_t (&o)[8]) __attribute__((always_inline)) {
     u32x4 wp[4], wo[4];
     uint32_t op[4], oo[4];
-    read_staged(((t & 1) * 4 + pwave) * TSZ, wp);
-    read_staged((8 + pwave) * TSZ, wo);
+    read_staged(((t & 1) * NH + pwave) * TSZ, wp);
+    read_staged((NW + pwave) * TSZ, wo);
     staged_offsets(row0 + 32 * pwave, t * BN, t >= 0 && t < pwtiles, op);
     staged_offsets(row0 + 32 * wave, t * BN, t >= 0 && t < wtiles, oo);
 #pragma unroll
@@ -598,7 +604,7 @@ void fwd_kernel(const FwdParams p) {
         if constexpr (MODE == kFwdScores) {
           if (vec) {
             if (loader) {
-              stage_tile((stage * 4 + wave) * TSZ, s, masked);
+              stage_tile((stage * NH + wave) * TSZ, s, masked);
             } else {
               // The storer reads this tile back row-major in the next key
               // tile (staged_pair), from other lanes of the same wave.  A
@@ -608,7 +614,7 @@ void fwd_kernel(const FwdParams p) {
               // closing lds_barrier (an asm with a memory clobber) keeps the
               // writes before the next iteration's read-back.
               __builtin_amdgcn_wave_barrier();
-              stage_tile((8 + pwave) * TSZ, s, masked);
+              stage_tile((NW + pwave) * TSZ, s, masked);
             }
           } else if (row_ok) {
             uint16_t* sr = p.scores + b * p.ss0 + qh * p.ss1 + (int64_t)qpos * p.ss2;

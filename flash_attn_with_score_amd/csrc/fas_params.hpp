@@ -56,7 +56,10 @@ struct FwdParams {
   int pack;
   int pack_shift;    // log2(pack) when pack is 1, 2, 4 or 8 (the score writer's packings)
   int nrb;           // virtual row blocks per group of `pack` heads
+  int bm;            // rows per workgroup (32 per wave; the score writer takes 128 or 256)
   int vec_scores;    // scores rows 16-byte aligned and N % 8 == 0
+  int zero_self;     // score writer: 1 = a workgroup writes its own row block's zeros
+                     // (all workgroups run at once), 0 = its mirror row block's
   int vec_region;    // split % 4 == 0
   int dropout;       // 1: the dropout instances (modes other than kFwdRegion)
   DropParams drop;   // scale also applies in the key-split combine (1 without dropout)
