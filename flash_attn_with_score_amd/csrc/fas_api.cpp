@@ -720,7 +720,8 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
   // launches take 128-row blocks (4 waves): twice the workgroups, in two
   // rounds the mirror order balances (B1 H32 S1024: 45.7 -> 37.5 us; H16
   // S4096: 179 -> 145 us; H32 S2048: 94.3 -> 95.9 us).
-  if (pw.pack == 1 &&
+  // (The dropout instances exist with 256-row blocks only.)
+  if (pw.pack == 1 && !(a->dropout_p > 0.f) &&
       (int64_t)pr.B * pr.H * ((pr.M + fas::kFwdRows - 1) / fas::kFwdRows) <= device_cu_count())
     bm = fas::kFwdRows / 2;
   fas::FwdParams p = fwd_params(a, pw, false, bm);

@@ -14,6 +14,11 @@ hipError_t launch_fwd_scores_packed(const FwdParams& p, int dtype, int d, hipStr
 // GQA-packed launches (p.pack > 1) take their own instances; the host never
 // packs a launch with dropout.
 hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, hipStream_t s) {
+  // Only the unpacked score writer without dropout has a 128-row instance;
+  // every other launch is built for 256-row blocks.
+  if (p.bm != kFwdRows && !(p.bm == kFwdRows / 2 && mode == kFwdScores && p.pack == 1 &&
+                            !p.dropout))
+    return hipErrorInvalidValue;
   if (p.pack > 1) {
     if (p.dropout && mode != kFwdRegion) return hipErrorInvalidValue;
     return mode == kFwdScores ? launch_fwd_scores_packed(p, dtype, d, s)
