@@ -195,11 +195,27 @@ fas::DropParams drop_params(const fas_attn_args* a, const Problem& pr) {
   fas::DropParams d{};
   d.scale = 1.f;
   if (!(a->dropout_p > 0.f)) return d;
-  d.offset = a->dropout_offset;
+  const uint64_t off = a->dropout_offset;
+  const bool wide = off >= (1ull << 31);  // a 64-bit offset fills counter word 1
   d.k0 = (uint32_t)a->dropout_seed;
   d.k1 = (uint32_t)(a->dropout_seed >> 32);
-  d.thresh = dropout_thresh(a->dropout_p);
-  d.wide = a->dropout_offset >= (1ull << 31) ? 1 : 0;
+  d.off_lo = (uint32_t)off;
+  // Index sums below 2^32 - off_lo do not carry into word 1; the element
+  // index stays below 2^31 with a 64-bit offset (the argument check rejects
+  // larger problems).
+  d.carry_lim = wide ? d.off_lo : 0u;
+  const uint32_t w1 = wide ? (uint32_t)(off >> 32) : 0u;
+  for (int c = 0; c < 2; ++c) {
+    const uint64_t pa = (uint64_t)fas::kPhiloxMulA * ((w1 + (uint32_t)c) ^ d.k0);
+    d.r1_hi[c] = (uint32_t)(pa >> 32) ^ (d.k1 + fas::kPhiloxWeylB);
+    d.r1_lo[c] = (uint32_t)pa;
+  }
+  // y = x ^ (x >> 31) > t (x the word as int32, t in [0, 2^31 - 1]) holds
+  // for x mod 2^32 in [t + 1, 2^32 - t - 2]: t + 1 .. 2^31 - 1 as x >= 0,
+  // 2^31 .. 2^32 - t - 2 as x <= -t - 2.  Empty for t = 2^31 - 1.
+  const uint32_t t = (uint32_t)dropout_thresh(a->dropout_p);
+  d.keep_lo = t + 1u;
+  d.keep_span = 0xFFFFFFFEu - 2u * t;
   d.n = pr.N;
   return d;
 }

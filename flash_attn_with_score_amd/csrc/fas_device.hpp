@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fas_params.hpp"
+
 namespace fas {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -175,41 +177,48 @@ __device__ __forceinline__ void buf_store16_nt(u32x4 v, __amdgpu_buffer_rsrc_t r
   __builtin_amdgcn_raw_buffer_store_b128(v, r, off, soff, kAuxNT);
 }
 
-// Philox4x32 with 6 rounds on counter (c0, c1, 0, 0) and key (k0, k1): the
-// first output word, i.e. Triton's randint(seed, offset, n_rounds=6)
-// (triton/language/random.py: philox_impl, randint4x), which follows the
-// Random123 Philox round: multipliers 0xD2511F53 / 0xCD9E8D57, key
-// increments 0x9E3779B9 / 0xBB67AE85 (Salmon et al., SC'11).  Each 32x32
-// product is one 64-bit multiply giving both halves; the unused parts of
-// the first and last rounds fold away.
-__device__ __forceinline__ uint32_t philox6_word0(uint32_t c0, uint32_t c1, uint32_t k0,
-                                                  uint32_t k1) {
-  uint32_t c2 = 0, c3 = 0;
-#pragma unroll
-  for (int r = 0; r < 6; ++r) {
-    const uint64_t pa = (uint64_t)0xD2511F53u * c0;
-    const uint64_t pb = (uint64_t)0xCD9E8D57u * c2;
-    const uint32_t n0 = (uint32_t)(pb >> 32) ^ c1 ^ k0;
-    const uint32_t n2 = (uint32_t)(pa >> 32) ^ c3 ^ k1;
-    c1 = (uint32_t)pb;
-    c3 = (uint32_t)pa;
-    c0 = n0;
-    c2 = n2;
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-  return c0;
+// a ^ b ^ c in one instruction (v_bitop3_b32; 0x96 is the truth table of the
+// three-way exclusive or over operand bytes 0xF0, 0xCC, 0xAA).
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+  return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
 }
-// Dropout keep decision for element index idx (mod 2^32).  Triton's uniform
-// is u = float(y) * 4.6566127342e-10 with y = x for x >= 0, -x - 1 (= ~x)
-// otherwise (x the random word as int32), and it keeps u > p.  u is
-// non-decreasing in y, so the host folds "u > p" into y > thresh.
+
+// Dropout keep decision for element index idx (mod 2^32): the first word of
+// Philox4x32-6 on counter (x0, w1, 0, 0) under key (k0, k1), i.e. Triton's
+// randint(seed, offset + idx, n_rounds=6) (triton/language/random.py:
+// philox_impl, randint4x), which follows the Random123 Philox round
+// (Salmon et al., SC'11): with products pa = A c0, pb = B c2,
+//   (c0, c1, c2, c3) <- (hi(pb) ^ c1 ^ k0, lo(pb), hi(pa) ^ c3 ^ k1, lo(pa)),
+// then the key advances by the Weyl increments.  Round 0's word-2 product is
+// zero and round 1's word-0 product is wave-uniform (DropParams), so a
+// weight costs 8 of the 12 products; each 32x32 product is one 64-bit
+// multiply giving both halves, and the parts the last rounds do not use fold
+// away.  Triton keeps the weight iff float(y) * 4.6566127342e-10 > p with
+// y = x for x >= 0 (x the word as int32), -x - 1 otherwise; the host turns
+// that into an interval of x mod 2^32.
 template <class DP>
 __device__ __forceinline__ bool dropout_keep(const DP& d, uint32_t idx) {
-  const uint64_t ctr = d.offset + idx;
-  const uint32_t x = philox6_word0((uint32_t)ctr, d.wide ? (uint32_t)(ctr >> 32) : 0u, d.k0, d.k1);
-  const int32_t y = (int32_t)(x ^ (uint32_t)((int32_t)x >> 31));
-  return y > d.thresh;
+  const uint32_t x0 = d.off_lo + idx;
+  const bool carry = x0 < d.carry_lim;
+  const uint64_t p0 = (uint64_t)kPhiloxMulA * x0;                                  // round 0
+  const uint64_t p1 = (uint64_t)kPhiloxMulB * ((uint32_t)(p0 >> 32) ^ d.k1);       // round 1
+  uint32_t c0 = (uint32_t)(p1 >> 32) ^ (d.k0 + kPhiloxWeylA);
+  uint32_t c1 = (uint32_t)p1;
+  uint32_t c2 = (carry ? d.r1_hi[1] : d.r1_hi[0]) ^ (uint32_t)p0;
+  uint32_t c3 = carry ? d.r1_lo[1] : d.r1_lo[0];
+  uint32_t k0 = d.k0 + 2u * kPhiloxWeylA, k1 = d.k1 + 2u * kPhiloxWeylB;
+#pragma unroll
+  for (int r = 2; r < 6; ++r) {
+    const uint64_t pa = (uint64_t)kPhiloxMulA * c0;
+    const uint64_t pb = (uint64_t)kPhiloxMulB * c2;
+    c0 = xor3((uint32_t)(pb >> 32), c1, k0);
+    c2 = xor3((uint32_t)(pa >> 32), c3, k1);
+    c1 = (uint32_t)pb;
+    c3 = (uint32_t)pa;
+    k0 += kPhiloxWeylA;
+    k1 += kPhiloxWeylB;
+  }
+  return c0 - d.keep_lo < d.keep_span;
 }
 
 // Row permutation applied to MFMA operand rows (bits 2 and 3 swapped).  With

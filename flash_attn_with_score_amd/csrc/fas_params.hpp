@@ -18,13 +18,27 @@ enum FwdMode : int {
 // *M + i)*N + j, n_rounds=6) > p (attention_with_scores.py:70-75, 173-176).
 // The index is taken mod 2^32 (the reference's int32 arithmetic) and the
 // counter's high word is used only for offsets >= 2^31 (a 64-bit offset).
+//
+// tl.rand is Philox4x32-6 on counter (x0, w1, 0, 0): x0 = (offset + index)
+// mod 2^32, w1 = 0 for an int32 offset, else the offset's high word plus the
+// carry of that sum.  Round 0 multiplies word 2 = 0, so it leaves (w1 ^ k0,
+// 0, hi(A x0) ^ k1, lo(A x0)); round 1's word-0 product A (w1 ^ k0) then
+// takes one of two wave-uniform values, which the host supplies.
+constexpr uint32_t kPhiloxMulA = 0xD2511F53u;   // word 0 multiplier
+constexpr uint32_t kPhiloxMulB = 0xCD9E8D57u;   // word 2 multiplier
+constexpr uint32_t kPhiloxWeylA = 0x9E3779B9u;  // key word 0 increment
+constexpr uint32_t kPhiloxWeylB = 0xBB67AE85u;  // key word 1 increment
 struct DropParams {
-  uint64_t offset;  // Philox offset of element (0, 0, 0, 0)
-  uint32_t k0, k1;  // Philox key: the seed's low and high words
-  int32_t thresh;   // keep iff the folded random word (as int32) > thresh
-  int wide;         // 1: counter word 1 = high word of offset + index
-  int n;            // N of the element index
-  float scale;      // O multiplier: 1/(1-p) where the reference rescales, else 1
+  uint32_t off_lo;     // offset mod 2^32: x0 = off_lo + index
+  uint32_t carry_lim;  // w1 is w1[1] iff x0 < carry_lim (the sum carried), else w1[0]
+  uint32_t k0, k1;     // Philox key: the seed's low and high words
+  uint32_t r1_hi[2];   // hi(A (w1 ^ k0)) ^ (k1 + kPhiloxWeylB), per value of w1
+  uint32_t r1_lo[2];   // lo(A (w1 ^ k0))
+  // Keep iff (word 0 - keep_lo) mod 2^32 < keep_span: Triton's uniform of
+  // word x exceeds p exactly on an interval of x mod 2^32 (host-made).
+  uint32_t keep_lo, keep_span;
+  int n;               // N of the element index
+  float scale;         // O multiplier: 1/(1-p) where the reference rescales, else 1
 };
 
 struct FwdParams {

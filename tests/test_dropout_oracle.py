@@ -78,3 +78,57 @@ def test_keep_mask_index():
     m64 = philox.keep_mask(seed, big, p, 0, 0, range(M), N, H, M)
     lo = philox.keep_mask(seed, 9, p, 0, 0, range(M), N, H, M)
     assert not np.array_equal(m64, lo)
+
+
+def test_keep_interval_form():
+    """The kernels test "uniform(x) > p" as (x - (t + 1)) mod 2^32 <
+    2^32 - 2t - 2, t the largest y whose uniform is <= p: the same decision
+    as Triton's folding y = x or -x - 1 (x as int32), over the words where
+    the two could part (around 0, +-t, 2^31) and random ones."""
+    rng = np.random.default_rng(7)
+    for p in (1e-6, 0.1, 0.5, 0.9, 0.999):
+        # t by bisection over fp32 uniforms, as the host computes it.
+        lo, hi = 0, 2**31 - 1
+        while hi - lo > 1:
+            mid = (lo + hi) // 2
+            if philox.uniform(np.uint32(mid)) <= np.float32(p):
+                lo = mid
+            else:
+                hi = mid
+        t = lo
+        edges = [0, 1, 2**31 - 1, 2**31, 2**32 - 1, t, t + 1, t + 2, 2**32 - t - 3,
+                 2**32 - t - 2, 2**32 - t - 1, 2**32 - t]
+        x = np.concatenate([np.array([e % 2**32 for e in edges], dtype=np.uint64),
+                            rng.integers(0, 2**32, size=20000, dtype=np.uint64)])
+        want = philox.uniform(x.astype(np.uint32)) > np.float32(p)
+        got = ((x - np.uint64(t + 1)) % np.uint64(2**32)) < np.uint64(2**32 - 2 * t - 2)
+        assert np.array_equal(got, want), p
+
+
+def test_split_first_rounds():
+    """The kernels' Philox-6 on counter (x0, w1, 0, 0): round 0's word-2
+    product is zero and round 1's word-0 product A (w1 ^ k0) is precomputed
+    per value of w1 (w1 = offset high word + carry of offset + index).  The
+    split form gives Philox's word 0 for both values of the carry."""
+    rng = np.random.default_rng(3)
+    key = (0x89ABCDEF, 0x01234567)
+    mask = 0xFFFFFFFF
+    for w1 in (0, 5, 0x7FFFFFFF):
+        x0 = rng.integers(0, 2**32, size=4096, dtype=np.uint64)
+        want = philox.philox4x32((x0, np.uint64(w1), 0, 0), key, 6)[0].astype(np.uint64)
+        pa1 = philox.M_A * ((w1 ^ key[0]) & mask)
+        p0 = np.uint64(philox.M_A) * x0
+        p1 = np.uint64(philox.M_B) * ((p0 >> np.uint64(32)) ^ np.uint64(key[1]))
+        c0 = (p1 >> np.uint64(32)) ^ np.uint64((key[0] + philox.W_A) & mask)
+        c1 = p1 & np.uint64(mask)
+        c2 = np.uint64((pa1 >> 32) ^ ((key[1] + philox.W_B) & mask)) ^ (p0 & np.uint64(mask))
+        c3 = np.uint64(pa1 & mask)
+        c3 = np.broadcast_to(c3, x0.shape)
+        k0, k1 = (key[0] + 2 * philox.W_A) & mask, (key[1] + 2 * philox.W_B) & mask
+        for _ in range(4):
+            pa = np.uint64(philox.M_A) * c0
+            pb = np.uint64(philox.M_B) * c2
+            c0, c1, c2, c3 = ((pb >> np.uint64(32)) ^ c1 ^ np.uint64(k0), pb & np.uint64(mask),
+                              (pa >> np.uint64(32)) ^ c3 ^ np.uint64(k1), pa & np.uint64(mask))
+            k0, k1 = (k0 + philox.W_A) & mask, (k1 + philox.W_B) & mask
+        assert np.array_equal(c0, want), w1

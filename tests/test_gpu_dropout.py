@@ -46,7 +46,11 @@ def _ceil4(x):
     return (x + 3) // 4 * 4
 
 
-@pytest.mark.parametrize("offset", [0, 123456, 2**31 + 1000], ids=["zero", "small", "wide"])
+# Offsets >= 2^31 are 64-bit: counter word 1 is the high word of offset +
+# index, which carries inside the tensor for the "carry" offsets.
+@pytest.mark.parametrize("offset", [0, 123456, 2**31 + 1000, 2**32 - 3000, 5 * 2**32 + 2**31,
+                                    7 * 2**32 - 10000],
+                         ids=["zero", "small", "wide", "carry", "wide_hi", "carry_hi"])
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
 @pytest.mark.parametrize("ep", ["attention_with_scores", "attention_with_row_sum"])
 def test_keep_mask_bit_exact(ep, offset, causal, gpu):
@@ -79,10 +83,22 @@ SHAPES = [(1, 4, 2, 200, 200, 64), (2, 3, 1, 130, 300, 128), (1, 4, 2, 32, 2048,
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "B{}H{}K{}M{}N{}D{}".format(*s))
 @pytest.mark.parametrize("ep", EPS)
 def test_entry_points_with_dropout(ep, shape, causal, dtype, gpu):
+    _check_entry_point(ep, shape, causal, dtype, 4096 * (1 + shape[0]), gpu)
+
+
+@pytest.mark.parametrize("ep", ["attention_with_scores", "attention_with_softmax_col_sum",
+                                "attention_cross_token_softmax_sum"])
+def test_entry_points_wide_offset_carry(ep, gpu):
+    """A 64-bit offset whose index sum carries into counter word 1 halfway
+    through the tensor (forward and column-pass masks)."""
+    _check_entry_point(ep, (1, 4, 2, 200, 200, 64), True, torch.float16, 2**32 - 77000, gpu)
+
+
+def _check_entry_point(ep, shape, causal, dtype, offset, gpu):
     B, Hq, Hk, M, N, D = shape
     split = N // 2 if "cross" in ep else None
-    seed, offset = 2024 + len(ep), 4096 * (1 + B)
-    print(f"[case] dropout {ep} {shape} causal={causal} {dtype}", flush=True)
+    seed = 2024 + len(ep)
+    print(f"[case] dropout {ep} {shape} causal={causal} {dtype} offset={offset}", flush=True)
     q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=11)
     _set_state(gpu, seed, offset)
     fn = getattr(fas, ep)
@@ -122,10 +138,20 @@ def test_attention_dropout(shape, dtype, gpu):
     """attention(): O with dropout and the 1/(1-p) rescale, L as without
     dropout, (seed, offset) returned, and dq, dk, dv through the same mask
     (flash.py:653-731, 843-895) against the fp64 oracle."""
+    _check_attention(shape, dtype, 640, gpu)
+
+
+def test_attention_dropout_wide_offset_carry(gpu):
+    """The backward kernels' masks with a 64-bit offset whose index sum
+    carries into counter word 1 inside the tensor."""
+    _check_attention((1, 4, 2, 200, 264, 64), torch.float16, 2**32 - 100000, gpu)
+
+
+def _check_attention(shape, dtype, offset, gpu):
     B, H, Hk, M, N, D = shape
-    print(f"[case] attention dropout {shape} {dtype}", flush=True)
+    print(f"[case] attention dropout {shape} {dtype} offset={offset}", flush=True)
     q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=dtype, seed=8)
-    seed, offset = 31337, 640
+    seed = 31337
     _set_state(gpu, seed, offset)
     qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
     o, L, tot, s, off = fas.attention(qd, kd, vd, causal=True, dropout_p=P,
