@@ -83,6 +83,22 @@ def test_plain_entry_points(ep, shape, dtype, causal, gpu):
     _run(ep, shape, dtype, causal, gpu)
 
 
+# The score writer without a causal mask: many key tiles, several row blocks
+# and head groups, GQA, and N a multiple of the 64-key tile.
+NONCAUSAL_SCORE_SHAPES = [
+    (2, 8, 4, 300, 1024, 128),
+    (1, 4, 4, 600, 768, 64),
+    (1, 12, 3, 513, 320, 32),
+    (3, 2, 2, 64, 4096, 16),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("shape", NONCAUSAL_SCORE_SHAPES, ids=_label)
+def test_scores_noncausal_many_tiles(shape, dtype, gpu):
+    _run("attention_with_scores", shape, dtype, False, gpu, seed=4)
+
+
 # Short query ranges against long key ranges: fewer row blocks than CUs, so
 # the plain and row-sum forward split each row block's keys over several
 # workgroups and merge fp32 partials (including rows with no key, M > N).
