@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import struct
 import threading
 from pathlib import Path
 
@@ -76,23 +77,27 @@ def strides3(t: torch.Tensor):
     return _I64x3(*t.stride())
 
 
+# AttnArgs as one packed record (the C struct has no padding), so that a
+# call fills it with a single pack instead of ~30 ctypes field writes.
+_ARGS_PACK = struct.Struct("<iifi6q4Q16qfiQQ")
+assert _ARGS_PACK.size == ctypes.sizeof(AttnArgs) and AttnArgs.dropout_offset.offset == 240
+
+
 def make_args(q, k, v, o, causal: bool, sm_scale: float, dropout=None) -> AttnArgs:
     """dropout: None, or (dropout_p, seed, offset) of the reference's stream."""
     B, H, M, D = q.shape
-    a = AttnArgs()
-    a.dtype = DTYPE_CODES[q.dtype]
-    a.causal = 1 if causal else 0
-    a.sm_scale = float(sm_scale)
-    a.batch, a.heads_q, a.seqlen_q, a.head_dim = B, H, M, D
-    a.heads_k, a.seqlen_k = k.shape[1], k.shape[2]
-    a.q, a.k, a.v, a.out = q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr()
-    a.q_stride, a.k_stride, a.v_stride, a.out_stride = (
-        strides4(q), strides4(k), strides4(v), strides4(o))
-    if dropout is not None:
-        a.dropout_p = float(dropout[0])
-        a.dropout_seed = int(dropout[1]) & 0xFFFFFFFFFFFFFFFF
-        a.dropout_offset = int(dropout[2]) & 0xFFFFFFFFFFFFFFFF
-    return a
+    if dropout is None:
+        dp, seed, offset = 0.0, 0, 0
+    else:
+        dp = float(dropout[0])
+        seed = int(dropout[1]) & 0xFFFFFFFFFFFFFFFF
+        offset = int(dropout[2]) & 0xFFFFFFFFFFFFFFFF
+    return AttnArgs.from_buffer_copy(_ARGS_PACK.pack(
+        DTYPE_CODES[q.dtype], 1 if causal else 0, float(sm_scale), 0,
+        B, H, k.shape[1], M, k.shape[2], D,
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+        *q.stride(), *k.stride(), *v.stride(), *o.stride(),
+        dp, 0, seed, offset))
 
 
 _P = ctypes.POINTER

@@ -331,3 +331,24 @@ def test_dropout_p_checked_in_python():
     for bad in (1.0, -0.1):
         with pytest.raises(ValueError, match="dropout_p"):
             _common.check_device_inputs(t, t, t, bad)
+
+
+def test_make_args_packs_every_field():
+    """make_args fills struct fas_attn_args with one packed record: every
+    field reads back as written, including strides of views, negative
+    sm_scale and 64-bit dropout seed and offset."""
+    q = torch.empty(2, 100, 6, 64, dtype=torch.bfloat16).transpose(1, 2)
+    k = torch.empty(2, 3, 70, 64, dtype=torch.bfloat16)
+    v = torch.empty(2, 3, 70, 64, dtype=torch.bfloat16)
+    o = torch.empty(2, 6, 100, 64, dtype=torch.bfloat16)
+    a = _native.make_args(q, k, v, o, True, -0.25, (0.1, 2**63 + 5, 2**40 + 7))
+    assert (a.dtype, a.causal, a.sm_scale, a.reserved) == (1, 1, -0.25, 0)
+    assert (a.batch, a.heads_q, a.heads_k, a.seqlen_q, a.seqlen_k, a.head_dim) == (
+        2, 6, 3, 100, 70, 64)
+    assert (a.q, a.k, a.v, a.out) == (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr())
+    assert tuple(a.q_stride) == q.stride() and tuple(a.k_stride) == k.stride()
+    assert tuple(a.v_stride) == v.stride() and tuple(a.out_stride) == o.stride()
+    assert a.dropout_p == pytest.approx(0.1) and a.reserved2 == 0
+    assert (a.dropout_seed, a.dropout_offset) == (2**63 + 5, 2**40 + 7)
+    b = _native.make_args(o, k, v, o, False, 0.5)
+    assert (b.dtype, b.causal, b.dropout_p, b.dropout_seed, b.dropout_offset) == (1, 0, 0.0, 0, 0)
