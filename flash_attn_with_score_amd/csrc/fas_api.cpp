@@ -87,6 +87,7 @@ uint32_t slice_bytes(int64_t rows, int64_t row_stride, int64_t D) {
 
 struct Problem {
   int B, H, Hk, G, M, N, D, dtype, causal;
+  bool dropout;  // dropout_p > 0
   float sm_scale;
   int pack;  // query heads per forward workgroup (GQA packing): G, or 1
 };
@@ -144,6 +145,7 @@ int check_shape(const char* fn, const fas_attn_args* a, Problem* pr) {
   pr->D = (int)D;
   pr->dtype = a->dtype;
   pr->causal = a->causal;
+  pr->dropout = a->dropout_p > 0.f;
   pr->sm_scale = a->sm_scale;
   pr->pack = choose_pack(a, pr->G, pr->M);
   return FAS_OK;
@@ -205,11 +207,16 @@ fas::DropParams drop_params(const fas_attn_args* a, const Problem& pr) {
   // larger problems).
   d.carry_lim = wide ? d.off_lo : 0u;
   const uint32_t w1 = wide ? (uint32_t)(off >> 32) : 0u;
+  uint32_t hi[2], lo[2];
   for (int c = 0; c < 2; ++c) {
     const uint64_t pa = (uint64_t)fas::kPhiloxMulA * ((w1 + (uint32_t)c) ^ d.k0);
-    d.r1_hi[c] = (uint32_t)(pa >> 32) ^ (d.k1 + fas::kPhiloxWeylB);
-    d.r1_lo[c] = (uint32_t)pa;
+    hi[c] = (uint32_t)(pa >> 32) ^ (d.k1 + fas::kPhiloxWeylB);
+    lo[c] = (uint32_t)pa;
   }
+  d.r1_hi = hi[0];
+  d.r1_hi_carry = hi[0] ^ hi[1];
+  d.r1_lo = lo[0];
+  d.r1_lo_carry = lo[0] ^ lo[1];
   // y = x ^ (x >> 31) > t (x the word as int32, t in [0, 2^31 - 1]) holds
   // for x mod 2^32 in [t + 1, 2^32 - t - 2]: t + 1 .. 2^31 - 1 as x >= 0,
   // 2^31 .. 2^32 - t - 2 as x <= -t - 2.  Empty for t = 2^31 - 1.
@@ -291,6 +298,8 @@ struct SplitPlan {
 
 struct Workspace {
   size_t lse = 0, part = 0, bsum = 0, region = 0, total = 0;  // byte offsets / total
+  size_t bits = 0;                                              // dropout keep bits
+  bool has_bits = false;
   size_t nl = 0, delta = 0;                                     // backward row values
   size_t so = 0, sm = 0, sl = 0, sr = 0;                        // key-split partials
   bool has_lse = false, has_part = false, has_bsum = false, has_region = false;
@@ -389,6 +398,19 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
       w.has_part = true;
       w.part = off;
       off += align256((size_t)pr.B * pr.H * ncols * 4);
+    }
+  }
+  // The softmax column sum with dropout: the forward stores its keep
+  // decisions (one bit per pair, 32-row words) for the column pass, which
+  // would otherwise evaluate the Philox stream again, when they fit the
+  // budget and a head's words stay below 2 GiB (32-bit buffer offsets).
+  if (variant == FAS_VARIANT_SOFTMAX_COL_SUM && pr.dropout) {
+    const size_t head_bytes = (size_t)((pr.M + 31) / 32) * pr.N * 4;
+    const size_t bytes = align256((size_t)pr.B * pr.H * head_bytes);
+    if (head_bytes < ((size_t)1 << 31) && off + bytes <= budget) {
+      w.has_bits = true;
+      w.bits = off;
+      off += bytes;
     }
   }
   if (variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED) {
@@ -533,14 +555,15 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
 
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   p.lse2 = at<float>(ws, w.lse);
+  if (w.has_bits) p.drop_bits = at<uint32_t>(ws, w.bits);
   if (!buffered) apply_split(p, w, ws);
   if (buffered) {
     p.region = at<float>(ws, w.region);
     p.split = (int)split;
     p.vec_region = (split % 4 == 0) ? 1 : 0;
   }
-  if ((rc = run_fwd(fn, p, pr, buffered ? fas::kFwdRegion : fas::kFwdPlain, stream)))
-    return rc;
+  const int mode = buffered ? fas::kFwdRegion : w.has_bits ? fas::kFwdPlainKeepBits : fas::kFwdPlain;
+  if ((rc = run_fwd(fn, p, pr, mode, stream))) return rc;
   if ((int64_t)pr.B * pr.Hk * ncols == 0) return FAS_OK;
   if ((int64_t)pr.B * pr.H * pr.M == 0) return zero_out3(fn, out, st, pr.B, pr.Hk, ncols, stream);
 
@@ -564,8 +587,9 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   c.qk_scale = p.qk_scale;
   // Only the softmax column sum masks its weights; the cross-token pass
   // does not (attention_cross_token_softmax_sum.py has no dropout there).
-  c.dropout = variant == FAS_VARIANT_SOFTMAX_COL_SUM ? p.dropout : 0;
+  c.dropout = variant == FAS_VARIANT_SOFTMAX_COL_SUM && p.dropout ? (w.has_bits ? 2 : 1) : 0;
   c.drop = p.drop;
+  c.drop_bits = p.drop_bits;
   float* part = nullptr;
   if (pr.G > 1) {
     part = at<float>(ws, w.part);

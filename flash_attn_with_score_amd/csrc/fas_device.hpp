@@ -11,6 +11,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "fas_params.hpp"
 
 namespace fas {
@@ -152,6 +154,29 @@ __device__ __forceinline__ void dma16(i32x4 rsrc, uint32_t voff, uint32_t lds_ba
 
 __device__ __forceinline__ void vm_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, in order.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+// Lanes L0 and L1 of w take the wave-uniform values x0 and x1
+// (v_writelane_b32).  x0 and x1 are typically a ballot just written by a
+// vector compare; the compiler's hazard checks do not look into inline
+// assembly, so the s_nop supplies the wait states between that write and
+// the lane writes (without it a lane was measured to receive a stale
+// register).
+template <int L0, int L1>
+__device__ __forceinline__ void write_lanes(uint32_t& w, uint32_t x0, uint32_t x1) {
+  static_assert(L0 >= 0 && L0 < 64 && L1 >= 0 && L1 < 64, "lane out of range");
+  asm volatile("s_nop 4\n\tv_writelane_b32 %0, %1, %3\n\tv_writelane_b32 %0, %2, %4"
+               : "+v"(w)
+               : "s"(x0), "s"(x1), "n"(L0), "n"(L1));
+}
+
 // Workgroup barrier ordering LDS only.  __syncthreads() is also a release
 // fence for global memory, which makes every wave drain its outstanding
 // global stores at each barrier.
@@ -196,9 +221,12 @@ __device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
 // zero and round 1's word-0 product is wave-uniform (DropParams), so a
 // weight costs 8 of the 12 products; each 32x32 product is one 64-bit
 // multiply giving both halves, and the parts the last rounds do not use fold
-// away.  Triton keeps the weight iff float(y) * 4.6566127342e-10 > p with
-// y = x for x >= 0 (x the word as int32), -x - 1 otherwise; the host turns
-// that into an interval of x mod 2^32.
+// away.  The carry picks round 1's product through a select against zero of
+// the host-made difference (one instruction per half; the uniform low half
+// joins round 2's key).  Triton keeps the weight iff
+// float(y) * 4.6566127342e-10 > p with y = x for x >= 0 (x the word as
+// int32), -x - 1 otherwise; the host turns that into an interval of
+// x mod 2^32.
 template <class DP>
 __device__ __forceinline__ bool dropout_keep(const DP& d, uint32_t idx) {
   const uint32_t x0 = d.off_lo + idx;
@@ -207,11 +235,21 @@ __device__ __forceinline__ bool dropout_keep(const DP& d, uint32_t idx) {
   const uint64_t p1 = (uint64_t)kPhiloxMulB * ((uint32_t)(p0 >> 32) ^ d.k1);       // round 1
   uint32_t c0 = (uint32_t)(p1 >> 32) ^ (d.k0 + kPhiloxWeylA);
   uint32_t c1 = (uint32_t)p1;
-  uint32_t c2 = (carry ? d.r1_hi[1] : d.r1_hi[0]) ^ (uint32_t)p0;
-  uint32_t c3 = carry ? d.r1_lo[1] : d.r1_lo[0];
+  uint32_t c2 = xor3(d.r1_hi, (uint32_t)p0, carry ? d.r1_hi_carry : 0u);
+  uint32_t c3 = carry ? d.r1_lo_carry : 0u;  // round 1's low half without d.r1_lo
   uint32_t k0 = d.k0 + 2u * kPhiloxWeylA, k1 = d.k1 + 2u * kPhiloxWeylB;
+  {  // round 2, taking d.r1_lo with its key
+    const uint64_t pa = (uint64_t)kPhiloxMulA * c0;
+    const uint64_t pb = (uint64_t)kPhiloxMulB * c2;
+    c0 = xor3((uint32_t)(pb >> 32), c1, k0);
+    c2 = xor3((uint32_t)(pa >> 32), c3, k1 ^ d.r1_lo);
+    c1 = (uint32_t)pb;
+    c3 = (uint32_t)pa;
+    k0 += kPhiloxWeylA;
+    k1 += kPhiloxWeylB;
+  }
 #pragma unroll
-  for (int r = 2; r < 6; ++r) {
+  for (int r = 3; r < 6; ++r) {
     const uint64_t pa = (uint64_t)kPhiloxMulA * c0;
     const uint64_t pb = (uint64_t)kPhiloxMulB * c2;
     c0 = xor3((uint32_t)(pb >> 32), c1, k0);

@@ -267,7 +267,7 @@ void fwd_kernel(const FwdParams p) {
 
   // Split over keys: the plain and row-sum modes may give a row block to
   // nsplit workgroups, each over its own share of the key tiles.
-  constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdRowSum;
+  constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdPlainKeepBits || MODE == kFwdRowSum;
   int rb, grp, split = 0;
   {
     int bid = blockIdx.x;
@@ -522,16 +522,39 @@ void fwd_kernel(const FwdParams p) {
   // after the row sum has taken them (attention_with_scores.py:169-176).
   // Weight e of pb[cs] is key k0 + 16cs + 8g + e of this lane's row.
   const uint32_t drow = ((uint32_t)bh * (uint32_t)p.M + (uint32_t)qpos) * (uint32_t)p.drop.n;
+  // Keep bits for the softmax column pass (kFwdPlainKeepBits): the wave's
+  // 32 rows of one key form one word.  A ballot of a keep decision gives
+  // two: lanes 0-31 (g = 0) hold rows 0-31 of key k, lanes 32-63 the same
+  // rows of key k + 8.  Lane L collects the word of key k0 + L and stores it
+  // (keys past N are not stored: a row-word's keys are its pitch).
+  constexpr bool kBits = MODE == kFwdPlainKeepBits;
+  static_assert(!kBits || DROP, "keep bits exist only with dropout");
+  __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
+  uint32_t wbase = 0;
+  if constexpr (kBits) {
+    const int r32 = (p.M + 31) >> 5;
+    rbits = make_rsrc(p.drop_bits + (int64_t)(b * p.H + h0) * r32 * p.N,
+                      __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)r32 * p.N * 4)));
+    wbase = (uint32_t)(wrow0 >> 5) * (uint32_t)p.N;
+  }
   auto drop_p = [&](u32x4 (&pb)[4], int k0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int cs = 0; cs < 4; ++cs)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t i0 = drow + (uint32_t)(k0 + 16 * cs + 8 * g + 2 * w);
-        const uint32_t m = (dropout_keep(p.drop, i0) ? 0xFFFFu : 0u) |
-                           (dropout_keep(p.drop, i0 + 1) ? 0xFFFF0000u : 0u);
-        pb[cs][w] &= m;
+    uint32_t word = 0;
+    static_for<16>([&](auto step) __attribute__((always_inline)) {
+      constexpr int cs = decltype(step)::value >> 2, w = decltype(step)::value & 3;
+      const uint32_t i0 = drow + (uint32_t)(k0 + 16 * cs + 8 * g + 2 * w);
+      const bool k_a = dropout_keep(p.drop, i0), k_b = dropout_keep(p.drop, i0 + 1);
+      pb[cs][w] &= (k_a ? 0xFFFFu : 0u) | (k_b ? 0xFFFF0000u : 0u);
+      if constexpr (kBits) {
+        const uint64_t ba = __builtin_amdgcn_ballot_w64(k_a);
+        const uint64_t bb = __builtin_amdgcn_ballot_w64(k_b);
+        constexpr int L = 16 * cs + 2 * w;
+        write_lanes<L, L + 8>(word, (uint32_t)ba, (uint32_t)(ba >> 32));
+        write_lanes<L + 1, L + 9>(word, (uint32_t)bb, (uint32_t)(bb >> 32));
       }
+    });
+    if (kBits && wrow0 < p.M)
+      __builtin_amdgcn_raw_buffer_store_b32(
+          word, rbits, k0 + lane < p.N ? (wbase + (uint32_t)(k0 + lane)) * 4u : kOffNone, 0, 0);
   };
   auto pv_mma = [&](const u32x4 (&pb)[4], const uint16_t* vt) __attribute__((always_inline)) {
 #pragma unroll
@@ -861,7 +884,7 @@ void fwd_kernel(const FwdParams p) {
     const float lse2 = m_ref * p.qk_scale + log2f_fast(l_tot);
     if (p.lse2 != nullptr) p.lse2[(int64_t)bh * p.M + qpos] = l_tot > 0.f ? lse2 : pos_inf();
     // attention()'s log normalizer m * sm_scale + ln(l) (flash.py:477-483).
-    if constexpr (MODE == kFwdPlain)
+    if constexpr (MODE == kFwdPlain || MODE == kFwdPlainKeepBits)
       if (p.lse_ln != nullptr)
         p.lse_ln[b * p.sl0 + qh * p.sl1 + (int64_t)qpos * p.sl2] =
             l_tot > 0.f ? lse2 * 0.69314718055994531f : neg_inf();
@@ -914,7 +937,7 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdParams p) {
   if (ch == 0) {
     const float lse2 = mx + log2f_fast(l);
     if (p.lse2 != nullptr) p.lse2[(int64_t)bh * p.M + row] = l > 0.f ? lse2 : pos_inf();
-    if constexpr (MODE == kFwdPlain)
+    if constexpr (MODE == kFwdPlain || MODE == kFwdPlainKeepBits)
       if (p.lse_ln != nullptr)
         p.lse_ln[b * p.sl0 + h * p.sl1 + (int64_t)row * p.sl2] =
             l > 0.f ? lse2 * 0.69314718055994531f : neg_inf();
@@ -925,14 +948,15 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdParams p) {
 
 template <class E, int D, int MODE, int NW, bool DROP, bool PACK>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
-  constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdRowSum;
+  constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdPlainKeepBits || MODE == kFwdRowSum;
   const int64_t nsplit = kCanSplit ? p.nsplit : 1;
   const dim3 grid((unsigned)((int64_t)p.nrb * (p.B * p.H / p.pack) * nsplit)), block(NW * 64);
   hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW, DROP, PACK>), grid, block, 0, stream, p);
   if constexpr (kCanSplit) {
     if (p.nsplit > 1 && p.M > 0) {
       const int64_t nblk = (p.M + 2048 / D - 1) / (2048 / D);
-      hipLaunchKernelGGL((fwd_combine_kernel<E, D, MODE>),
+      constexpr int CM = MODE == kFwdPlainKeepBits ? kFwdPlain : MODE;
+      hipLaunchKernelGGL((fwd_combine_kernel<E, D, CM>),
                          dim3((unsigned)(nblk * p.B * p.H)), dim3(256), 0, stream, p);
     }
   }

@@ -10,7 +10,8 @@ enum FwdMode : int {
   kFwdPlain = 0,   // output (+ optional base-2 LSE)
   kFwdScores = 1,  // + (B,H,M,N) scaled scores, masked -> 0
   kFwdRowSum = 2,  // + (B,H,M) row sums of scaled scores
-  kFwdRegion = 3   // + fp32 raw scores of rows >= split, keys < split
+  kFwdRegion = 3,  // + fp32 raw scores of rows >= split, keys < split
+  kFwdPlainKeepBits = 4  // kFwdPlain with dropout, storing the keep decisions (drop_bits)
 };
 
 // Dropout of the attention weights with the reference's random stream:
@@ -32,8 +33,10 @@ struct DropParams {
   uint32_t off_lo;     // offset mod 2^32: x0 = off_lo + index
   uint32_t carry_lim;  // w1 is w1[1] iff x0 < carry_lim (the sum carried), else w1[0]
   uint32_t k0, k1;     // Philox key: the seed's low and high words
-  uint32_t r1_hi[2];   // hi(A (w1 ^ k0)) ^ (k1 + kPhiloxWeylB), per value of w1
-  uint32_t r1_lo[2];   // lo(A (w1 ^ k0))
+  // Round 1's word-0 product A (w1 ^ k0) for w1 without the carry, and the
+  // exclusive or of each half with its value for w1 with the carry:
+  uint32_t r1_hi, r1_hi_carry;  // hi(A (w1 ^ k0)) ^ (k1 + kPhiloxWeylB)
+  uint32_t r1_lo, r1_lo_carry;  // lo(A (w1 ^ k0))
   // Keep iff (word 0 - keep_lo) mod 2^32 < keep_span: Triton's uniform of
   // word x exceeds p exactly on an interval of x mod 2^32 (host-made).
   uint32_t keep_lo, keep_span;
@@ -77,6 +80,10 @@ struct FwdParams {
   int vec_region;    // split % 4 == 0
   int dropout;       // 1: the dropout instances (modes other than kFwdRegion)
   DropParams drop;   // scale also applies in the key-split combine (1 without dropout)
+  // kFwdPlainKeepBits: the keep decisions as bits for the softmax column
+  // pass, word ((b*H + h) * ceil(M/32) + i/32) * N + j holding rows
+  // 32*(i/32) .. +31 of key j (bit i % 32).
+  uint32_t* drop_bits;
   // Split over keys (kFwdPlain, kFwdRowSum): nsplit workgroups per row block,
   // each taking tps key tiles and writing fp32 partials at row pitch Mpad
   // (= nrb * rows per workgroup); a combine pass merges them.
@@ -116,8 +123,10 @@ struct ColsmParams {
   int causal, causal_off;
   int nkb;               // key blocks
   float qk_scale;        // |sm_scale| * log2(e)
-  int dropout;           // 1: weights pass through the dropout mask
+  int dropout;           // 1: weights pass through the dropout mask (Philox), 2: through
+                         // the forward's keep bits (drop_bits, FwdParams layout)
   DropParams drop;
+  const uint32_t* drop_bits;
 };
 
 // Raw-score column sums by linearity: sum_i (q_i . k_j) = (sum_i q_i) . k_j.

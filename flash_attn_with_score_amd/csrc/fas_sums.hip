@@ -9,11 +9,13 @@ static hipError_t colsm_t(const ColsmParams& p, hipStream_t s) {
   // One workgroup per mirror pair of key blocks.
   const dim3 grid((unsigned)((int64_t)((p.nkb + 1) / 2) * p.B * p.H));
   if (p.lse_ln != nullptr)
-    hipLaunchKernelGGL((colsm64_kernel<E, D, true, false>), grid, dim3(512), 0, s, p);
+    hipLaunchKernelGGL((colsm64_kernel<E, D, true, 0>), grid, dim3(512), 0, s, p);
+  else if (p.dropout == 2)
+    hipLaunchKernelGGL((colsm64_kernel<E, D, false, 2>), grid, dim3(512), 0, s, p);
   else if (p.dropout)
-    hipLaunchKernelGGL((colsm64_kernel<E, D, false, true>), grid, dim3(512), 0, s, p);
+    hipLaunchKernelGGL((colsm64_kernel<E, D, false, 1>), grid, dim3(512), 0, s, p);
   else
-    hipLaunchKernelGGL((colsm64_kernel<E, D, false, false>), grid, dim3(512), 0, s, p);
+    hipLaunchKernelGGL((colsm64_kernel<E, D, false, 0>), grid, dim3(512), 0, s, p);
   return hipGetLastError();
 }
 

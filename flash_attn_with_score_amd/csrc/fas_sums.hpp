@@ -27,6 +27,9 @@
 
 namespace fas {
 
+// Byte offset past every buffer extent: the load returns 0.
+constexpr uint32_t kOffNoneSums = 0x80000000u;
+
 // ---------------------------------------------------------------- softmax
 
 __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb, int& bh) {
@@ -66,9 +69,12 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
 // total_attention) instead of the forward's base-2 LSE; a template flag so
 // the default copy carries no conversion code in its loop.
 // DROP: the weights pass through the dropout mask before the sum, as the
-// reference's column pass does (attention_with_col_softmax_sum.py:237-244).
+// reference's column pass does (attention_with_col_softmax_sum.py:237-244):
+// 1 evaluates the mask's Philox stream again, 2 reads the keep bits the
+// forward pass stored (one word per key and 32-row block, prefetched with
+// the next step's Q rows).
 // The sign of a negative sm_scale is applied to K once per block.
-template <class E, int D, bool LN, bool DROP>
+template <class E, int D, bool LN, int DROP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void colsm64_kernel(const ColsmParams p) {
   constexpr int KS = D / 16;
@@ -97,6 +103,12 @@ void colsm64_kernel(const ColsmParams p) {
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
   const float* lse = p.lse2 + (int64_t)bh * p.M;
   const int t1 = (p.M + TQ - 1) / TQ;
+  __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
+  if constexpr (DROP == 2) {
+    const int r32 = (p.M + 31) >> 5;
+    rbits = make_rsrc(p.drop_bits + (int64_t)bh * r32 * p.N,
+                      __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)r32 * p.N * 4)));
+  }
 
   u32x4 qst[CPT];
   float lst = 0.f;
@@ -161,15 +173,35 @@ void colsm64_kernel(const ColsmParams p) {
     const int t0 = max(0, rstart) / TQ;
 
     float colacc[2] = {0.f, 0.f};
+    // Keep words of step t (DROP == 2): block (qb, j) is rows
+    // t*TQ + 64 rg + 32 qb .. +31 of key key0 + 32 j + c.
+    uint32_t bcur[4] = {0u, 0u, 0u, 0u}, bnext[4] = {0u, 0u, 0u, 0u};
+    auto fetch_bits = [&](int t, uint32_t (&w)[4]) __attribute__((always_inline)) {
+      if constexpr (DROP == 2) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const int key = key0 + 32 * j + c;
+            const uint32_t rw = (uint32_t)((t * TQ + 64 * rg + 32 * qb) >> 5);
+            w[2 * qb + j] = __builtin_amdgcn_raw_buffer_load_b32(
+                rbits, key < p.N ? (rw * (uint32_t)p.N + (uint32_t)key) * 4u : kOffNoneSums, 0, 0);
+          }
+      }
+    };
     if (t0 < t1) {
       fetch(t0);
+      fetch_bits(t0, bcur);
       stash(0);
     }
     __syncthreads();
     auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
       constexpr int stage = decltype(stage_tag)::value;
       const bool more = t + 1 < t1;
-      if (more) fetch(t + 1);
+      if (more) {
+        fetch(t + 1);
+        fetch_bits(t + 1, bnext);
+      }
       const int r0 = t * TQ + 64 * rg;  // this row group's first row
       const uint16_t* qt = qlds[stage];
 #pragma unroll
@@ -225,11 +257,15 @@ void colsm64_kernel(const ColsmParams p) {
                 const int row = rq0 + acc_row(r, g);
                 if (p.causal_off + row < key0 + 32 * j + c) s[j][r] = 0.f;
               }
-              if constexpr (DROP) {
+              if constexpr (DROP == 1) {
                 const uint32_t row = (uint32_t)(rq0 + acc_row(r, g));
                 const uint32_t idx = ((uint32_t)bh * (uint32_t)p.M + row) * (uint32_t)p.drop.n +
                                      (uint32_t)(key0 + 32 * j + c);
                 if (!dropout_keep(p.drop, idx)) s[j][r] = 0.f;
+              }
+              if constexpr (DROP == 2) {
+                // Bit acc_row(r, g) = 16 (r / 8) + 8 g + r % 8 of the block's word.
+                if (!((bcur[2 * qb + j] >> (8 * g + 16 * (r >> 3) + (r & 7))) & 1u)) s[j][r] = 0.f;
               }
             }
 #pragma unroll
@@ -244,7 +280,11 @@ void colsm64_kernel(const ColsmParams p) {
           else body(std::true_type{});
         }
       }
-      if (more) stash(stage ^ 1);
+      if (more) {
+        stash(stage ^ 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bcur[i] = bnext[i];
+      }
       __syncthreads();
     };
     for (int t = t0; t < t1; t += 2) {

@@ -176,3 +176,40 @@ def _check_attention(shape, dtype, offset, gpu):
     assert_out_close(og, r["out"])
     for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
         assert_out_close(got, r[name])
+
+
+def test_softmax_col_sum_keep_bits_match_philox(gpu):
+    """The softmax column sum with dropout stores the forward pass's keep
+    decisions as bits for its column pass.  The no-allocation entry point,
+    whose 64 MiB scratch cannot hold them at this size, evaluates the Philox
+    stream again instead: both routes must give identical bits, here with a
+    64-bit offset whose index sum carries into counter word 1."""
+    import ctypes
+
+    from flash_attn_with_score_amd import _native
+
+    B, H, M, N, D = 1, 8, 8192, 8192, 64
+    print(f"[case] keep bits vs Philox B{B}H{H}M{M}N{N}D{D}", flush=True)
+    lib = _native.load()
+    q, k, v = inputs.make_qkv(B, H, H, M, N, D, dtype=torch.float16, seed=12, device=gpu)
+    drop = (P, 4321, 2**32 - 5_000_000)
+    stream = torch.cuda.current_stream().cuda_stream
+    o_bits = torch.empty_like(q)
+    c_bits = torch.empty((B, H, N), dtype=torch.float32, device=gpu)
+    a = _native.make_args(q, k, v, o_bits, True, D ** -0.5, drop)
+    nbytes = lib.fas_workspace_bytes(_native.VARIANT_SOFTMAX_COL_SUM, ctypes.byref(a), 0)
+    assert nbytes > 64 << 20  # room for the keep bits
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=gpu)
+    wptr = ws.data_ptr() + (-ws.data_ptr()) % 256
+    rc = lib.fas_attention_with_softmax_col_sum(ctypes.byref(a), c_bits.data_ptr(),
+                                                _native.strides3(c_bits), wptr, nbytes, stream)
+    _native.check(lib, rc, "fas_attention_with_softmax_col_sum")
+    o_phx = torch.full_like(q, float("nan"))
+    c_phx = torch.full((B, H, N), float("nan"), dtype=torch.float32, device=gpu)
+    a2 = _native.make_args(q, k, v, o_phx, True, D ** -0.5, drop)
+    rc = lib.fas_attention_with_softmax_col_sum_noalloc(ctypes.byref(a2), c_phx.data_ptr(),
+                                                        _native.strides3(c_phx), stream)
+    _native.check(lib, rc, "fas_attention_with_softmax_col_sum_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(o_bits, o_phx)
+    assert torch.equal(c_bits, c_phx)
