@@ -430,6 +430,14 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
       w.part = off;
       off += align256((size_t)pr.B * pr.H * pr.N * 2 * pr.D * 4);
     }
+    // With dropout the dK/dV kernel stores its keep decisions (one bit per
+    // pair) for the dQ kernel, when a head's words stay below 2 GiB.
+    const size_t head_bytes = (size_t)bwd_mpad(pr) * ((pr.N + 31) / 32) * 4;
+    if (pr.dropout && head_bytes < ((size_t)1 << 31)) {
+      w.has_bits = true;
+      w.bits = off;
+      off += align256((size_t)pr.B * pr.H * head_bytes);
+    }
   }
   if (raw) {
     const int64_t row_lo = variant == FAS_VARIANT_CROSS_QK_SUM ? split : 0;
@@ -995,6 +1003,8 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   p.nrb = p.Mpad / fas::kBwdBlock;
   p.nprep = (p.Mpad + (2048 / pr.D) - 1) / (2048 / pr.D);
   p.partial = bwd_partial(pr) ? 1 : 0;
+  p.n32 = (pr.N + 31) / 32;
+  if (w.has_bits) p.drop_bits = at<uint32_t>(ws, w.bits);
   p.sm_scale = std::fabs(pr.sm_scale);
   p.scale_signed = pr.sm_scale;
   p.qk_scale = qk_scale_of(pr.sm_scale);

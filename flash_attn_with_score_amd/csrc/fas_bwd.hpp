@@ -39,6 +39,9 @@
 namespace fas {
 
 constexpr float kLog2e = 1.44269504088896341f;
+// Byte offset past every buffer extent: the access is dropped (store) or
+// reads 0 (load).
+constexpr uint32_t kOffNoneBwd = 0x80000000u;
 
 // Packs accumulator registers 8cs..8cs+7 (contraction indices 8g..8g+7 of
 // k-step cs) as an MFMA B operand.
@@ -159,9 +162,14 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
   const float qk = p.qk_scale;
   const uint32_t q_base = lds_addr(&qlds[0][0]), g_base = lds_addr(&glds[0][0]);
 
+  const bool bits = DROP && p.drop_bits != nullptr;
   for (int hh = 0; hh < nheads && t0 < t1; ++hh) {
     const int h = h0 + hh;
     const int64_t bh = (int64_t)b * p.H + h;
+    __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
+    if (bits)
+      rbits = make_rsrc(p.drop_bits + bh * p.Mpad * p.n32,
+                        __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)p.Mpad * p.n32 * 4)));
     const i32x4 wq = make_rsrc_words(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
     const i32x4 wg = make_rsrc_words(p.dout + b * p.sg0 + h * p.sg1, p.g_bytes);
     const float* nlg = p.nl + bh * p.Mpad;
@@ -227,17 +235,47 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
           for (int r = 0; r < 16; ++r)
             if (acc_row(r, g) < lim) pr[r] = 0.f;
         }
+        if constexpr (DROP) {
+          // Keep bits for the dQ kernel (p.drop_bits): the ballot of
+          // register r's keep decisions is the block's keys for rows
+          // acc_row(r, 0) (lanes 0-31) and acc_row(r, 1) (lanes 32-63);
+          // lane L collects row r0 + L's word and lanes 0-31 store them.
+          // The keep decisions come first, all 16 Philox evaluations free to
+          // interleave; the lane writes (inline assembly, which the compiler
+          // does not move instructions across) follow in their own pass.
+          bool keep[16];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if constexpr (DROP) {
+          for (int r = 0; r < 16; ++r) {
             const uint32_t idx =
                 ((uint32_t)bh * (uint32_t)p.M + (uint32_t)(r0 + acc_row(r, g))) *
                     (uint32_t)p.N + (uint32_t)(key0 + c);
-            const bool keep = dropout_keep(p.drop, idx);
+            keep[r] = dropout_keep(p.drop, idx);
             const float nd = xlds[stage][32 * qb + acc_row(r, g)];  // -delta
-            s[r] = keep ? pr[r] : 0.f;
-            dp[r] = pr[r] * ((keep ? p.drop.scale * dp[r] : 0.f) + nd);
-          } else {
+            s[r] = keep[r] ? pr[r] : 0.f;
+            dp[r] = pr[r] * ((keep[r] ? p.drop.scale * dp[r] : 0.f) + nd);
+          }
+          uint32_t word = 0;
+          if (bits) {
+            // Registers r .. r+3 (acc_row(r, 0) = 16 (r / 8) + r % 8) per
+            // group of four ballots.
+            static_for<4>([&](auto qi) __attribute__((always_inline)) {
+              constexpr int r = 4 * decltype(qi)::value;
+              constexpr int L = 16 * (r >> 3) + (r & 7);
+              const uint64_t bk[4] = {__builtin_amdgcn_ballot_w64(keep[r]),
+                                      __builtin_amdgcn_ballot_w64(keep[r + 1]),
+                                      __builtin_amdgcn_ballot_w64(keep[r + 2]),
+                                      __builtin_amdgcn_ballot_w64(keep[r + 3])};
+              write_lanes8<L, L + 8, L + 1, L + 9, L + 2, L + 10, L + 3, L + 11>(word, bk);
+            });
+          }
+          if (bits && key0 < p.N)
+            __builtin_amdgcn_raw_buffer_store_b32(
+                word, rbits, lane < 32 ? (uint32_t)((r0 + lane) * p.n32 + (key0 >> 5)) * 4u
+                                       : kOffNoneBwd,
+                0, 0);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
             s[r] = pr[r];
             dp[r] = pr[r] * dp[r];
           }
@@ -418,15 +456,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const VtOff vto = vt_offsets<D>(lane);
   const uint32_t rco = row_chunk_offset<D>(perm_row(c), g);
 
+  // Keep words of tile t (dropout with p.drop_bits): this row's keys
+  // 64t .. 64t+31 and 64t+32 .. 64t+63, loaded with the tile's K and V.
+  const bool bits = DROP && p.drop_bits != nullptr;
+  __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
+  if (bits)
+    rbits = make_rsrc(p.drop_bits + (int64_t)bh * p.Mpad * p.n32,
+                      __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)p.Mpad * p.n32 * 4)));
+  uint32_t wcur[2] = {0u, 0u}, wnext[2] = {0u, 0u};
+  auto fetch_bits = [&](int t, uint32_t (&w)[2]) __attribute__((always_inline)) {
+    if constexpr (DROP) {
+      if (bits) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int kw = 2 * t + j;
+          w[j] = __builtin_amdgcn_raw_buffer_load_b32(
+              rbits, kw < p.n32 ? (uint32_t)(qrow * p.n32 + kw) * 4u : kOffNoneBwd, 0, 0);
+        }
+      }
+    }
+  };
   if (ntiles > 0) {
     fetch(0, 0);
+    fetch_bits(0, wcur);
     vm_wait_all();
     __syncthreads();
   }
   auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
     constexpr int stage = decltype(stage_tag)::value;
     const bool more = t + 1 < ntiles;
-    if (more) fetch(t + 1, stage ^ 1);
+    if (more) {
+      fetch(t + 1, stage ^ 1);
+      fetch_bits(t + 1, wnext);
+    }
     const uint16_t* kt = klds[stage];
     const uint16_t* vt = vlds[stage];
     // One 32-key sub-block.  The mask (tiles at the diagonal or the key
@@ -470,16 +532,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       // Key kbase + acc_row(r, g) is admissible iff acc_row(r, g) < lim.
       const int lim = (p.causal ? min(p.N, p.causal_off + qrow + 1) : p.N) - kbase;
+      float pr[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float pr = exp2f_fast(fmaf(s[r], qk, nl));
-        if (!full && acc_row(r, g) >= lim) pr = 0.f;
-        if constexpr (DROP) {
-          const uint32_t idx = drow + (uint32_t)(kbase + acc_row(r, g));
-          dp[r] = pr * ((dropout_keep(p.drop, idx) ? p.drop.scale * dp[r] : 0.f) + xl);
+        pr[r] = exp2f_fast(fmaf(s[r], qk, nl));
+        if (!full && acc_row(r, g) >= lim) pr[r] = 0.f;
+      }
+      if constexpr (DROP) {
+        if (bits) {
+          // The dK/dV kernel's keep bits: bit acc_row(r, g) of the word of
+          // this row and sub-block.
+          const uint32_t wb = wcur[kb2] >> (8 * g);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const bool keep = (wb >> (16 * (r >> 3) + (r & 7))) & 1u;
+            dp[r] = pr[r] * ((keep ? p.drop.scale * dp[r] : 0.f) + xl);
+          }
         } else {
-          dp[r] = pr * dp[r];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t idx = drow + (uint32_t)(kbase + acc_row(r, g));
+            dp[r] = pr[r] * ((dropout_keep(p.drop, idx) ? p.drop.scale * dp[r] : 0.f) + xl);
+          }
         }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dp[r] = pr[r] * dp[r];
       }
       const u32x4 sb0 = pack_b<E>(dp, 0), sb1 = pack_b<E>(dp, 1);
       __builtin_amdgcn_sched_barrier(0);
@@ -507,7 +585,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (t * BN + 32 * kb2 < whi) body(kb2, t < tfull);
       }
     }
-    if (more) vm_wait_all();
+    if (more) {
+      vm_wait_all();
+      wcur[0] = wnext[0];
+      wcur[1] = wnext[1];
+    }
     __syncthreads();
   };
   for (int t = 0; t < ntiles; t += 2) {

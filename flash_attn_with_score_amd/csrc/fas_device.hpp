@@ -176,6 +176,22 @@ __device__ __forceinline__ void write_lanes(uint32_t& w, uint32_t x0, uint32_t x
                : "+v"(w)
                : "s"(x0), "s"(x1), "n"(L0), "n"(L1));
 }
+// Eight lanes at once, behind one s_nop: the 32-bit halves of four ballots
+// b[0..3] go to lanes L[2i] (low half) and L[2i + 1] (high half).
+template <int L0, int L1, int L2, int L3, int L4, int L5, int L6, int L7>
+__device__ __forceinline__ void write_lanes8(uint32_t& w, const uint64_t (&b)[4]) {
+  asm volatile(
+      "s_nop 4\n\t"
+      "v_writelane_b32 %0, %1, %9\n\tv_writelane_b32 %0, %2, %10\n\t"
+      "v_writelane_b32 %0, %3, %11\n\tv_writelane_b32 %0, %4, %12\n\t"
+      "v_writelane_b32 %0, %5, %13\n\tv_writelane_b32 %0, %6, %14\n\t"
+      "v_writelane_b32 %0, %7, %15\n\tv_writelane_b32 %0, %8, %16"
+      : "+v"(w)
+      : "s"((uint32_t)b[0]), "s"((uint32_t)(b[0] >> 32)), "s"((uint32_t)b[1]),
+        "s"((uint32_t)(b[1] >> 32)), "s"((uint32_t)b[2]), "s"((uint32_t)(b[2] >> 32)),
+        "s"((uint32_t)b[3]), "s"((uint32_t)(b[3] >> 32)), "n"(L0), "n"(L1), "n"(L2), "n"(L3),
+        "n"(L4), "n"(L5), "n"(L6), "n"(L7));
+}
 
 // Workgroup barrier ordering LDS only.  __syncthreads() is also a release
 // fence for global memory, which makes every wave drain its outstanding

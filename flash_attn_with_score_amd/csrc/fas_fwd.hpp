@@ -538,20 +538,32 @@ void fwd_kernel(const FwdParams p) {
     wbase = (uint32_t)(wrow0 >> 5) * (uint32_t)p.N;
   }
   auto drop_p = [&](u32x4 (&pb)[4], int k0) __attribute__((always_inline)) {
-    uint32_t word = 0;
-    static_for<16>([&](auto step) __attribute__((always_inline)) {
-      constexpr int cs = decltype(step)::value >> 2, w = decltype(step)::value & 3;
+    // The keep decisions first (32 independent Philox evaluations the
+    // compiler interleaves), then the lane writes in a pass of their own:
+    // instructions are not moved across inline assembly.
+    bool keep[32];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int cs = i >> 2, w = i & 3;
       const uint32_t i0 = drow + (uint32_t)(k0 + 16 * cs + 8 * g + 2 * w);
-      const bool k_a = dropout_keep(p.drop, i0), k_b = dropout_keep(p.drop, i0 + 1);
-      pb[cs][w] &= (k_a ? 0xFFFFu : 0u) | (k_b ? 0xFFFF0000u : 0u);
-      if constexpr (kBits) {
-        const uint64_t ba = __builtin_amdgcn_ballot_w64(k_a);
-        const uint64_t bb = __builtin_amdgcn_ballot_w64(k_b);
-        constexpr int L = 16 * cs + 2 * w;
-        write_lanes<L, L + 8>(word, (uint32_t)ba, (uint32_t)(ba >> 32));
-        write_lanes<L + 1, L + 9>(word, (uint32_t)bb, (uint32_t)(bb >> 32));
-      }
-    });
+      keep[2 * i] = dropout_keep(p.drop, i0);
+      keep[2 * i + 1] = dropout_keep(p.drop, i0 + 1);
+      pb[cs][w] &= (keep[2 * i] ? 0xFFFFu : 0u) | (keep[2 * i + 1] ? 0xFFFF0000u : 0u);
+    }
+    uint32_t word = 0;
+    if constexpr (kBits) {
+      // Keep pairs i and i + 1 (keys 16 cs + 2 w + {0, 1}, + 8 in the high
+      // halves) per group of four ballots.
+      static_for<8>([&](auto step) __attribute__((always_inline)) {
+        constexpr int i = 2 * decltype(step)::value;
+        constexpr int L = 16 * (i >> 2) + 2 * (i & 3);
+        const uint64_t bk[4] = {__builtin_amdgcn_ballot_w64(keep[2 * i]),
+                                __builtin_amdgcn_ballot_w64(keep[2 * i + 1]),
+                                __builtin_amdgcn_ballot_w64(keep[2 * i + 2]),
+                                __builtin_amdgcn_ballot_w64(keep[2 * i + 3])};
+        write_lanes8<L, L + 8, L + 1, L + 9, L + 2, L + 10, L + 3, L + 11>(word, bk);
+      });
+    }
     if (kBits && wrow0 < p.M)
       __builtin_amdgcn_raw_buffer_store_b32(
           word, rbits, k0 + lane < p.N ? (wbase + (uint32_t)(k0 + lane)) * 4u : kOffNone, 0, 0);
