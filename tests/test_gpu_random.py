@@ -126,3 +126,94 @@ def test_random_case(case, gpu):
         assert_scores_close(extra, ref_extra)
     else:
         assert_sum_close(extra, ref_extra, naive.ENTRY_POINT_OUTPUT[ep])
+
+
+# Dropout: the same sweep over the entry points that draw the mask, with the
+# generator state set to a seeded (seed, offset) -- a third of the offsets
+# 64-bit, some of them carrying into counter word 1 inside the tensor -- so
+# the keep-bit routes (softmax column sum, attention backward) and Philox
+# evaluated in place meet ragged shapes, GQA and every head dim.
+DROP_EPS = [
+    "attention_with_scores",
+    "attention_with_row_sum",
+    "attention_with_softmax_col_sum",
+    "attention_cross_token_softmax_sum",
+    "attention",
+]
+
+
+def _drop_cases(n: int = 60, seed: int = 7331):
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        ep = DROP_EPS[i % len(DROP_EPS)]
+        G = rng.choice([1, 1, 2, 4])
+        Hk = rng.choice([1, 2])
+        B = rng.choice([1, 2])
+        M = rng.choice([1, 33, 64, 100, 257, 390])
+        N = rng.choice([8, 63, 64, 65, 200, 512])
+        D = rng.choice([16, 32, 64, 128])
+        dtype = rng.choice(["f16", "bf16"])
+        causal = rng.random() < 0.6
+        total = B * Hk * G * M * N
+        kind = rng.choice(["small", "wide", "carry"])
+        if kind == "small":
+            offset = rng.randrange(0, 2**31 - total)
+        elif kind == "wide":
+            offset = rng.randrange(2**31, 2**40)
+        else:  # 64-bit, the low word wrapping inside the tensor
+            offset = (rng.randrange(1, 2**8) << 32) - rng.randrange(1, total)
+        offset &= ~3  # torch's generator keeps offsets at multiples of 4
+        split = rng.randint(1, min(M, N)) if "cross" in ep else None
+        out.append((i, ep, (B, Hk * G, Hk, M, N, D), dtype, causal, offset, split))
+    return out
+
+
+def _drop_label(case):
+    i, ep, (B, Hq, Hk, M, N, D), dtype, causal, offset, split = case
+    return (f"{i}-{ep}-B{B}H{Hq}K{Hk}M{M}N{N}D{D}-{dtype}-{'causal' if causal else 'full'}"
+            f"-o{offset}-x{split}")
+
+
+@pytest.mark.parametrize("case", _drop_cases(), ids=_drop_label)
+def test_random_dropout_case(case, gpu):
+    i, ep, shape, dname, causal, offset, split = case
+    B, Hq, Hk, M, N, D = shape
+    dtype = torch.float16 if dname == "f16" else torch.bfloat16
+    p_drop, seed = 0.2, 9000 + i
+    print(f"[case] {_drop_label(case)}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=2000 + i)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    gen = torch.cuda.default_generators[gpu.index or 0]
+    state = gen.get_state()
+    state.view(torch.int64)[0], state.view(torch.int64)[1] = seed, offset
+    gen.set_state(state)
+    dropout = (p_drop, seed, offset)
+
+    if ep == "attention":
+        g = torch.Generator("cpu").manual_seed(7)
+        do = torch.randn(B, Hq, M, D, generator=g).to(dtype)
+        qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (qd, kd, vd))
+        o = fas.attention(qg, kg, vg, causal=causal, dropout_p=p_drop)
+        dq, dk, dv = torch.autograd.grad(o, (qg, kg, vg), do.to(gpu))
+        torch.cuda.synchronize()
+        ref = naive.attention_reference(q, k, v, do, causal=causal, dropout=dropout)
+        assert_out_close(o, ref["out"])
+        assert_out_close(dq, ref["dq"], "dq")
+        assert_out_close(dk, ref["dk"], "dk")
+        assert_out_close(dv, ref["dv"], "dv")
+        return
+
+    fn = getattr(fas, ep)
+    if split is None:
+        out, extra = fn(qd, kd, vd, causal=causal, dropout_p=p_drop)
+    else:
+        out, extra = fn(qd, kd, vd, split, causal=causal, dropout_p=p_drop)
+    torch.cuda.synchronize()
+    ref_out, ref_extra = naive.oracle_for(ep, q, k, v, causal=causal, split=split,
+                                          dropout=dropout)
+    assert_out_close(out, ref_out)
+    if naive.ENTRY_POINT_OUTPUT[ep] == "scores":
+        assert_scores_close(extra, ref_extra)
+    else:
+        assert_sum_close(extra, ref_extra, naive.ENTRY_POINT_OUTPUT[ep])
