@@ -14,6 +14,9 @@
 //   kFwdRegion  + raw fp32 scores of the region rows >= split, keys < split
 //               (masked -> -inf), the first pass of the buffered cross-token
 //               softmax sum (attention_cross_token_softmax_sum.py:539-552)
+//   kFwdPlainKeepBits
+//               kFwdPlain with dropout, + the keep decisions as bits for the
+//               softmax column pass (which then need not evaluate Philox)
 //
 // Design (MI355X-first):
 //  * Workgroup = NW wave64s, 32 query rows per wave, BM = 32*NW rows; key
