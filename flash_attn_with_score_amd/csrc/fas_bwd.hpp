@@ -270,8 +270,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
           }
           if (bits && key0 < p.N)
             __builtin_amdgcn_raw_buffer_store_b32(
-                word, rbits, lane < 32 ? (uint32_t)((r0 + lane) * p.n32 + (key0 >> 5)) * 4u
-                                       : kOffNoneBwd,
+                word, rbits,
+                lane < 32 ? (uint32_t)((((r0 >> 5) * p.n32 + (key0 >> 5)) << 5) + lane) * 4u
+                          : kOffNoneBwd,
                 0, 0);
         } else {
 #pragma unroll
@@ -471,7 +472,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int j = 0; j < 2; ++j) {
           const int kw = 2 * t + j;
           w[j] = __builtin_amdgcn_raw_buffer_load_b32(
-              rbits, kw < p.n32 ? (uint32_t)(qrow * p.n32 + kw) * 4u : kOffNoneBwd, 0, 0);
+              rbits, kw < p.n32 ? (uint32_t)((((wrow0 >> 5) * p.n32 + kw) << 5) + c) * 4u
+                                : kOffNoneBwd,
+              0, 0);
         }
       }
     }

@@ -184,8 +184,9 @@ struct BwdParams {
   int dropout;           // 1: the dropout instances (flash.py:653-659, 705-731, 843-890)
   DropParams drop;       // scale = 1/(1-p)
   // Optional with dropout: the dK/dV kernel stores its keep decisions for
-  // the dQ kernel, word ((b*H + h) * Mpad + i) * n32 + j/32 holding keys
-  // 32*(j/32) .. +31 of row i (bit j % 32); null: dQ evaluates Philox.
+  // the dQ kernel, word (((b*H + h) * Mpad/32 + i/32) * n32 + j/32) * 32 +
+  // i % 32 holding keys 32*(j/32) .. +31 of row i (bit j % 32): the 32 rows
+  // of a block are consecutive words; null: dQ evaluates Philox.
   uint32_t* drop_bits;
   int n32;               // ceil(N / 32)
 };
