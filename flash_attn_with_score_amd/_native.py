@@ -14,7 +14,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -35,6 +35,7 @@ VARIANT_CROSS_SOFTMAX_SUM = 6
 VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7
 VARIANT_ATTENTION_BACKWARD = 8
 VARIANT_ATTENTION_FORWARD = 9
+VARIANT_KEEP_BITS = 10  # size of the keep_bits buffer (fas_attn_args.keep_bits)
 
 _I64x4 = ctypes.c_int64 * 4
 _I64x3 = ctypes.c_int64 * 3
@@ -66,6 +67,7 @@ class AttnArgs(ctypes.Structure):
         ("reserved2", ctypes.c_int32),
         ("dropout_seed", ctypes.c_uint64),
         ("dropout_offset", ctypes.c_uint64),
+        ("keep_bits", ctypes.c_void_p),
     ]
 
 
@@ -79,12 +81,14 @@ def strides3(t: torch.Tensor):
 
 # AttnArgs as one packed record (the C struct has no padding), so that a
 # call fills it with a single pack instead of ~30 ctypes field writes.
-_ARGS_PACK = struct.Struct("<iifi6q4Q16qfiQQ")
-assert _ARGS_PACK.size == ctypes.sizeof(AttnArgs) and AttnArgs.dropout_offset.offset == 240
+_ARGS_PACK = struct.Struct("<iifi6q4Q16qfiQQQ")
+assert _ARGS_PACK.size == ctypes.sizeof(AttnArgs) and AttnArgs.keep_bits.offset == 248
 
 
-def make_args(q, k, v, o, causal: bool, sm_scale: float, dropout=None) -> AttnArgs:
-    """dropout: None, or (dropout_p, seed, offset) of the reference's stream."""
+def make_args(q, k, v, o, causal: bool, sm_scale: float, dropout=None,
+              keep_bits: int | None = 0) -> AttnArgs:
+    """dropout: None, or (dropout_p, seed, offset) of the reference's stream;
+    keep_bits: device address of the forward's keep-bit buffer, or 0 (None: 0)."""
     B, H, M, D = q.shape
     if dropout is None:
         dp, seed, offset = 0.0, 0, 0
@@ -97,7 +101,7 @@ def make_args(q, k, v, o, causal: bool, sm_scale: float, dropout=None) -> AttnAr
         B, H, k.shape[1], M, k.shape[2], D,
         q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
         *q.stride(), *k.stride(), *v.stride(), *o.stride(),
-        dp, 0, seed, offset))
+        dp, 0, seed, offset, keep_bits or 0))
 
 
 _P = ctypes.POINTER

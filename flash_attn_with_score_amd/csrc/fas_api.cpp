@@ -88,6 +88,7 @@ uint32_t slice_bytes(int64_t rows, int64_t row_stride, int64_t D) {
 struct Problem {
   int B, H, Hk, G, M, N, D, dtype, causal;
   bool dropout;  // dropout_p > 0
+  bool keep;     // dropout with a caller keep-bit buffer (fas_attn_args.keep_bits)
   float sm_scale;
   int pack;  // query heads per forward workgroup (GQA packing): G, or 1
 };
@@ -146,6 +147,7 @@ int check_shape(const char* fn, const fas_attn_args* a, Problem* pr) {
   pr->dtype = a->dtype;
   pr->causal = a->causal;
   pr->dropout = a->dropout_p > 0.f;
+  pr->keep = pr->dropout && a->keep_bits != nullptr;
   pr->sm_scale = a->sm_scale;
   pr->pack = choose_pack(a, pr->G, pr->M);
   return FAS_OK;
@@ -369,6 +371,38 @@ bool bwd_partial(const Problem& pr) {
   return pr.G > 1 && (int64_t)pr.B * pr.Hk * bwd_nkb(pr) < 256;
 }
 
+// The caller's keep-bit buffer (fas_attn_args.keep_bits) of attention's
+// forward and backward: key-major words for the dK/dV kernel (word
+// ((b*H + h) * ceil(M/32) + i/32) * N + j, bit i % 32), then 32-row blocks
+// of row-major words for the dQ kernel (the backward's own layout, rows
+// padded to Mpad).  Each head's part must stay below 2 GiB (32-bit buffer
+// offsets); otherwise no buffer is used.
+struct KeepLayout {
+  size_t keys = 0, rows = 0, total = 0;  // byte offsets / total
+  bool ok = false;
+};
+KeepLayout keep_layout(const Problem& pr) {
+  KeepLayout k;
+  const size_t head_keys = (size_t)((pr.M + 31) / 32) * pr.N * 4;
+  const size_t head_rows = (size_t)bwd_mpad(pr) * ((pr.N + 31) / 32) * 4;
+  if (!pr.dropout || head_keys >= ((size_t)1 << 31) || head_rows >= ((size_t)1 << 31)) return k;
+  k.keys = 0;
+  k.rows = align256((size_t)pr.B * pr.H * head_keys);
+  k.total = k.rows + align256((size_t)pr.B * pr.H * head_rows);
+  k.ok = true;
+  return k;
+}
+
+int check_keep(const char* fn, const fas_attn_args* a, const Problem& pr, KeepLayout* kl) {
+  *kl = keep_layout(pr);
+  if (!pr.keep) return FAS_OK;
+  if (!kl->ok)
+    return fail(FAS_ERR_UNSUPPORTED, fn, "keep_bits given, but a head's bits exceed 2 GiB");
+  if ((reinterpret_cast<uintptr_t>(a->keep_bits) & 255u) != 0)
+    return fail(FAS_ERR_INVALID, fn, "keep_bits must be 256-byte aligned");
+  return FAS_OK;
+}
+
 // Column count of a variant's side output.
 int64_t ncols_of(int variant, const Problem& pr, int64_t split) {
   switch (variant) {
@@ -433,7 +467,7 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
     // With dropout the dK/dV kernel stores its keep decisions (one bit per
     // pair) for the dQ kernel, when a head's words stay below 2 GiB.
     const size_t head_bytes = (size_t)bwd_mpad(pr) * ((pr.N + 31) / 32) * 4;
-    if (pr.dropout && head_bytes < ((size_t)1 << 31)) {
+    if (pr.dropout && !pr.keep && head_bytes < ((size_t)1 << 31)) {
       w.has_bits = true;
       w.bits = off;
       off += align256((size_t)pr.B * pr.H * head_bytes);
@@ -670,9 +704,9 @@ const char* fas_last_error(void) { return g_last_error.c_str(); }
 
 size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
   Problem pr;
-  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_ATTENTION_FORWARD)
-    return (size_t)-1;
+  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_KEEP_BITS) return (size_t)-1;
   if (check_shape("fas_workspace_bytes", a, &pr)) return (size_t)-1;
+  if (variant == FAS_VARIANT_KEEP_BITS) return keep_layout(pr).total;
   const bool has_split = variant == FAS_VARIANT_CROSS_QK_SUM ||
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM ||
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED;
@@ -895,6 +929,8 @@ int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3
   if ((rc = check_out3(fn, "lse", lse, st))) return rc;
   const Workspace w = layout(FAS_VARIANT_ATTENTION_FORWARD, pr, 0);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
+  KeepLayout kl;
+  if ((rc = check_keep(fn, a, pr, &kl))) return rc;
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   rescale_dropout(p, a);
   apply_split(p, w, ws);
@@ -902,7 +938,12 @@ int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3
   p.sl0 = st[0];
   p.sl1 = st[1];
   p.sl2 = st[2];
-  return run_fwd(fn, p, pr, fas::kFwdPlain, stream);
+  if (pr.keep) {
+    p.drop_bits = at<uint32_t>(a->keep_bits, kl.keys);
+    p.drop_rows = at<uint32_t>(a->keep_bits, kl.rows);
+    p.rows32 = (int)(bwd_mpad(pr) / 32);
+  }
+  return run_fwd(fn, p, pr, pr.keep ? fas::kFwdPlainKeepBits : fas::kFwdPlain, stream);
 }
 
 int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t lst[3],
@@ -962,6 +1003,8 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   }
   const Workspace w = layout(FAS_VARIANT_ATTENTION_BACKWARD, pr, 0);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
+  KeepLayout kl;
+  if ((rc = check_keep(fn, a, pr, &kl))) return rc;
   if (pr.M > (1 << 26)) return fail(FAS_ERR_UNSUPPORTED, fn, "seqlen_q exceeds 2^26");
 
   fas::BwdParams p{};
@@ -1005,6 +1048,11 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   p.partial = bwd_partial(pr) ? 1 : 0;
   p.n32 = (pr.N + 31) / 32;
   if (w.has_bits) p.drop_bits = at<uint32_t>(ws, w.bits);
+  if (pr.keep) {
+    // The forward's bits: dK/dV reads the key-major words, dQ the row blocks.
+    p.keep_keys = at<uint32_t>(a->keep_bits, kl.keys);
+    p.drop_bits = at<uint32_t>(a->keep_bits, kl.rows);
+  }
   p.sm_scale = std::fabs(pr.sm_scale);
   p.scale_signed = pr.sm_scale;
   p.qk_scale = qk_scale_of(pr.sm_scale);

@@ -162,14 +162,38 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
   const float qk = p.qk_scale;
   const uint32_t q_base = lds_addr(&qlds[0][0]), g_base = lds_addr(&glds[0][0]);
 
-  const bool bits = DROP && p.drop_bits != nullptr;
+  // With the forward's keep words (keep_keys) the mask is read, not
+  // evaluated, and nothing is stored for the dQ kernel; otherwise the
+  // decisions are evaluated and, with drop_bits, stored for it.
+  const bool from_keys = DROP && p.keep_keys != nullptr;
+  const bool bits = DROP && p.drop_bits != nullptr && !from_keys;
+  const int r32 = (p.M + 31) >> 5;
   for (int hh = 0; hh < nheads && t0 < t1; ++hh) {
     const int h = h0 + hh;
     const int64_t bh = (int64_t)b * p.H + h;
-    __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
+    __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0), rkeys = rbits;
     if (bits)
       rbits = make_rsrc(p.drop_bits + bh * p.Mpad * p.n32,
                         __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)p.Mpad * p.n32 * 4)));
+    if (from_keys)
+      rkeys = make_rsrc(p.keep_keys + bh * r32 * p.N,
+                        __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)r32 * p.N * 4)));
+    // Keep words of tile t (from_keys): rows t*TQ + 32 qb .. +31 of key
+    // key0 + c, loaded with the tile's Q and dO.
+    uint32_t kcur[2] = {0u, 0u}, knext[2] = {0u, 0u};
+    auto fetch_keys = [&](int t, uint32_t (&w)[2]) __attribute__((always_inline)) {
+      if constexpr (DROP) {
+        if (from_keys) {
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            const int key = key0 + c;
+            const uint32_t rw = (uint32_t)((t * TQ + 32 * qb) >> 5);
+            w[qb] = __builtin_amdgcn_raw_buffer_load_b32(
+                rkeys, key < p.N ? (rw * (uint32_t)p.N + (uint32_t)key) * 4u : kOffNoneBwd, 0, 0);
+          }
+        }
+      }
+    };
     const i32x4 wq = make_rsrc_words(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
     const i32x4 wg = make_rsrc_words(p.dout + b * p.sg0 + h * p.sg1, p.g_bytes);
     const float* nlg = p.nl + bh * p.Mpad;
@@ -192,13 +216,17 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
       }
     };
     fetch(t0, 0);
+    fetch_keys(t0, kcur);
     vm_wait_all();
     stash(0);
     __syncthreads();
     auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
       constexpr int stage = decltype(stage_tag)::value;
       const bool more = t + 1 < t1;
-      if (more) fetch(t + 1, stage ^ 1);
+      if (more) {
+        fetch(t + 1, stage ^ 1);
+        fetch_keys(t + 1, knext);
+      }
       const uint16_t* qt = qlds[stage];
       const uint16_t* gt = glds[stage];
       // One 32-row block.  The mask (diagonal blocks only) changes the
@@ -244,12 +272,22 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
           // interleave; the lane writes (inline assembly, which the compiler
           // does not move instructions across) follow in their own pass.
           bool keep[16];
+          if (from_keys) {
+            // Bit acc_row(r, g) = 16 (r / 8) + 8 g + r % 8 of the block's word.
+            const uint32_t wb = kcur[qb] >> (8 * g);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) keep[r] = (wb >> (16 * (r >> 3) + (r & 7))) & 1u;
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const uint32_t idx =
+                  ((uint32_t)bh * (uint32_t)p.M + (uint32_t)(r0 + acc_row(r, g))) *
+                      (uint32_t)p.N + (uint32_t)(key0 + c);
+              keep[r] = dropout_keep(p.drop, idx);
+            }
+          }
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const uint32_t idx =
-                ((uint32_t)bh * (uint32_t)p.M + (uint32_t)(r0 + acc_row(r, g))) *
-                    (uint32_t)p.N + (uint32_t)(key0 + c);
-            keep[r] = dropout_keep(p.drop, idx);
             const float nd = xlds[stage][32 * qb + acc_row(r, g)];  // -delta
             s[r] = keep[r] ? pr[r] : 0.f;
             dp[r] = pr[r] * ((keep[r] ? p.drop.scale * dp[r] : 0.f) + nd);
@@ -306,6 +344,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
       if (more) {
         vm_wait_all();
         stash(stage ^ 1);
+        kcur[0] = knext[0];
+        kcur[1] = knext[1];
       }
       __syncthreads();
     };

@@ -532,13 +532,18 @@ void fwd_kernel(const FwdParams p) {
   // (keys past N are not stored: a row-word's keys are its pitch).
   constexpr bool kBits = MODE == kFwdPlainKeepBits;
   static_assert(!kBits || DROP, "keep bits exist only with dropout");
-  __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
+  __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0), rrows = rbits;
   uint32_t wbase = 0;
   if constexpr (kBits) {
     const int r32 = (p.M + 31) >> 5;
     rbits = make_rsrc(p.drop_bits + (int64_t)(b * p.H + h0) * r32 * p.N,
                       __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)r32 * p.N * 4)));
     wbase = (uint32_t)(wrow0 >> 5) * (uint32_t)p.N;
+    if (p.drop_rows != nullptr) {
+      const int64_t head = (int64_t)p.rows32 * ((p.N + 31) >> 5) * 32;
+      rrows = make_rsrc(p.drop_rows + (int64_t)(b * p.H + h0) * head,
+                        __builtin_amdgcn_readfirstlane((uint32_t)(head * 4)));
+    }
   }
   auto drop_p = [&](u32x4 (&pb)[4], int k0) __attribute__((always_inline)) {
     // The keep decisions first (32 independent Philox evaluations the
@@ -570,6 +575,30 @@ void fwd_kernel(const FwdParams p) {
     if (kBits && wrow0 < p.M)
       __builtin_amdgcn_raw_buffer_store_b32(
           word, rbits, k0 + lane < p.N ? (wbase + (uint32_t)(k0 + lane)) * 4u : kOffNone, 0, 0);
+    if (kBits && p.drop_rows != nullptr) {
+      // The backward's row blocks: this row's keys k0 .. k0+31 and
+      // k0+32 .. k0+63 as two words.  Keep pair i holds keys
+      // 16 (i/4) + 8 g + 2 (i%4) + {0, 1}; each half-wave holds half of
+      // every word, the other half comes from lane l ^ 32.
+      uint32_t part[2] = {0u, 0u};
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int bit = 16 * ((i >> 2) & 1) + 8 * g + 2 * (i & 3);
+        part[i >> 3] |= (keep[2 * i] ? 1u << bit : 0u) | (keep[2 * i + 1] ? 2u << bit : 0u);
+      }
+      float lo0, hi0, lo1, hi1;
+      lane_halves(__builtin_bit_cast(float, part[0]), lo0, hi0);
+      lane_halves(__builtin_bit_cast(float, part[1]), lo1, hi1);
+      const uint32_t full =
+          g == 0 ? __builtin_bit_cast(uint32_t, lo0) | __builtin_bit_cast(uint32_t, hi0)
+                 : __builtin_bit_cast(uint32_t, lo1) | __builtin_bit_cast(uint32_t, hi1);
+      const int kw = (k0 >> 5) + g, n32 = (p.N + 31) >> 5;
+      __builtin_amdgcn_raw_buffer_store_b32(
+          full, rrows,
+          kw < n32 && wrow0 < p.M ? (uint32_t)((((wrow0 >> 5) * n32 + kw) << 5) + c) * 4u
+                                  : kOffNone,
+          0, 0);
+    }
   };
   auto pv_mma = [&](const u32x4 (&pb)[4], const uint16_t* vt) __attribute__((always_inline)) {
 #pragma unroll

@@ -80,10 +80,14 @@ struct FwdParams {
   int vec_region;    // split % 4 == 0
   int dropout;       // 1: the dropout instances (modes other than kFwdRegion)
   DropParams drop;   // scale also applies in the key-split combine (1 without dropout)
-  // kFwdPlainKeepBits: the keep decisions as bits for the softmax column
-  // pass, word ((b*H + h) * ceil(M/32) + i/32) * N + j holding rows
-  // 32*(i/32) .. +31 of key j (bit i % 32).
+  // kFwdPlainKeepBits: the keep decisions as bits, word
+  // ((b*H + h) * ceil(M/32) + i/32) * N + j holding rows 32*(i/32) .. +31
+  // of key j (bit i % 32); and, when drop_rows is set (attention's forward),
+  // again in the backward's row blocks, word
+  // (((b*H + h) * rows32 + i/32) * ceil(N/32) + j/32) * 32 + i % 32 (bit j % 32).
   uint32_t* drop_bits;
+  uint32_t* drop_rows;
+  int rows32;        // the backward's padded rows / 32
   // Split over keys (kFwdPlain, kFwdRowSum): nsplit workgroups per row block,
   // each taking tps key tiles and writing fp32 partials at row pitch Mpad
   // (= nrb * rows per workgroup); a combine pass merges them.
@@ -189,6 +193,11 @@ struct BwdParams {
   // of a block are consecutive words; null: dQ evaluates Philox.
   uint32_t* drop_bits;
   int n32;               // ceil(N / 32)
+  // The forward's key-major keep words (FwdParams.drop_bits layout), when
+  // the caller kept them: the dK/dV kernel reads them instead of evaluating
+  // Philox and does not write drop_bits (which then holds the forward's
+  // row blocks).
+  const uint32_t* keep_keys;
 };
 
 }  // namespace fas

@@ -30,12 +30,20 @@ def _check_inputs(q, k, v):
     assert q.shape[1] % Hk == 0, "number of heads in q must be a multiple of that in k & v"
 
 
-def _forward(q, k, v, causal, sm_scale, want_total, dropout_p):
+def _forward(q, k, v, causal, sm_scale, want_total, dropout_p, keep=False):
+    """keep: with dropout, store the mask's bits for the backward pass
+    (one bit per pair, in a buffer returned as (pointer, tensor))."""
     p = _common.finish_problem(q, k, v, sm_scale)
     o = _common.new_output(p.q)
     L = torch.empty((p.B, p.H, p.M), device=q.device, dtype=torch.float32)
     drop = _common.draw_dropout(p.q, p.k, dropout_p)
     args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale, drop)
+    kept = (0, None)
+    if keep and drop is not None:
+        kptr, _, kbuf = _common.workspace(_native.VARIANT_KEEP_BITS, args, 0, q.device)
+        if kbuf is not None:
+            args.keep_bits = kptr
+            kept = (kptr, kbuf)
     ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_FORWARD, args, 0,
                                              q.device)
     _common.call("fas_attention_forward", p.q, ctypes.byref(args), L.data_ptr(),
@@ -45,7 +53,7 @@ def _forward(q, k, v, causal, sm_scale, want_total, dropout_p):
         tot = torch.empty((p.B, p.H, p.N), device=q.device, dtype=torch.float32)
         _common.call("fas_total_attention", p.q, ctypes.byref(args), L.data_ptr(),
                      _native.strides3(L), tot.data_ptr(), _native.strides3(tot))
-    return p, o, L, tot, drop
+    return p, o, L, tot, drop, kept
 
 
 class FlashAttention(torch.autograd.Function):
@@ -57,12 +65,18 @@ class FlashAttention(torch.autograd.Function):
                 return_total_attention, return_seed_offset):
         _check_inputs(q, k, v)
         _common.check_device_inputs(q, k, v, dropout_p)
-        p, o, L, tot, drop = _forward(q, k, v, causal, sm_scale, return_total_attention,
-                                      dropout_p)
+        # With dropout the forward keeps the mask's bits (B*Hq*M*N/8 bytes in
+        # two layouts, ~N*M/4 bytes per head) so that the backward reads the
+        # mask instead of evaluating the random stream again; the reference
+        # regenerates it (flash.py:653-659), with the same result.
+        need_grad = any(ctx.needs_input_grad[:3])
+        p, o, L, tot, drop, kept = _forward(q, k, v, causal, sm_scale, return_total_attention,
+                                            dropout_p, keep=need_grad)
         ctx.save_for_backward(p.q, p.k, p.v, o, L)
         ctx.sm_scale = p.sm_scale
         ctx.causal = causal
         ctx.drop = drop
+        ctx.keep_ptr, ctx.keep_buf = kept
         if return_log_normalizer or return_total_attention or return_seed_offset:
             # seed and offset only with dropout and return_seed_offset
             # (flash.py:161-169).
@@ -81,8 +95,10 @@ class FlashAttention(torch.autograd.Function):
         dq = _common.new_output(q)
         dk = torch.empty((B, Hk, N, D), dtype=k.dtype, device=q.device)
         dv = torch.empty((B, Hk, N, D), dtype=v.dtype, device=q.device)
-        # The forward's (p, seed, offset): the same keep mask (flash.py:653-659).
-        args = _native.make_args(q, k, v, o, ctx.causal, ctx.sm_scale, ctx.drop)
+        # The forward's (p, seed, offset): the same keep mask (flash.py:653-659),
+        # read from the forward's bits when it kept them.
+        args = _native.make_args(q, k, v, o, ctx.causal, ctx.sm_scale, ctx.drop,
+                                 ctx.keep_ptr if ctx.keep_buf is not None else 0)
         ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args, 0,
                                                  q.device)
         _common.call("fas_attention_backward", q, ctypes.byref(args), do.data_ptr(),

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FAS_ABI_VERSION 6
+#define FAS_ABI_VERSION 7
 
 typedef enum fas_dtype {
   FAS_DTYPE_F16 = 0,
@@ -75,7 +75,9 @@ typedef enum fas_variant {
   FAS_VARIANT_CROSS_SOFTMAX_SUM = 6,
   FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED = 7,
   FAS_VARIANT_ATTENTION_BACKWARD = 8,
-  FAS_VARIANT_ATTENTION_FORWARD = 9
+  FAS_VARIANT_ATTENTION_FORWARD = 9,
+  /* Not a workspace: the size of the keep_bits buffer below. */
+  FAS_VARIANT_KEEP_BITS = 10
 } fas_variant;
 
 /* The attention problem shared by every entry point.  Strides are in
@@ -108,11 +110,20 @@ typedef struct fas_attn_args {
    * softmax sum, the scores-only call, the total attention and the score and
    * raw-sum outputs ignore it.  Offsets >= 2^31 with B*Hq*M*N >= 2^31 return
    * FAS_ERR_UNSUPPORTED.  fas_attention_backward takes the forward's dropout
-   * fields and regenerates the same mask. */
+   * fields and regenerates the same mask, or reads it from keep_bits. */
   float dropout_p;
   int32_t reserved2;
   uint64_t dropout_seed;
   uint64_t dropout_offset;
+  /* Optional, with dropout: a device buffer of
+   * fas_workspace_bytes(FAS_VARIANT_KEEP_BITS, ...) bytes, 256-byte aligned,
+   * owned by the caller.  fas_attention_forward stores the mask in it (one
+   * bit per pair, in the two layouts the backward kernels read);
+   * fas_attention_backward given the same buffer and dropout fields reads
+   * it instead of evaluating the random stream again.  NULL: both evaluate
+   * the stream.  The other entry points ignore it.  This build's own
+   * addition: the reference's backward regenerates the mask. */
+  void* keep_bits;
 } fas_attn_args;
 
 int fas_abi_version(void);

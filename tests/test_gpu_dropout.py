@@ -12,6 +12,8 @@ ignoring dropout.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -213,3 +215,51 @@ def test_softmax_col_sum_keep_bits_match_philox(gpu):
     torch.cuda.synchronize()
     assert torch.equal(o_bits, o_phx)
     assert torch.equal(c_bits, c_phx)
+
+
+@pytest.mark.parametrize("shape", [(1, 4, 2, 200, 264, 64), (2, 3, 3, 97, 1000, 128)],
+                         ids=lambda s: "B{}H{}K{}M{}N{}D{}".format(*s))
+def test_attention_keep_bits_match_philox(shape, gpu):
+    """attention()'s forward stores the keep bits for its backward
+    (keep_bits); a backward without them (keep_bits = 0) evaluates the
+    Philox stream in its dK/dV kernel instead.  Both routes must give the
+    same O and the same dq, dk, dv bit for bit, here with a 64-bit offset
+    whose index sum carries into counter word 1."""
+    from flash_attn_with_score_amd import _common, _native
+
+    B, H, Hk, M, N, D = shape
+    print(f"[case] attention keep bits vs Philox {shape}", flush=True)
+    lib = _native.load()
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=torch.float16, seed=14, device=gpu)
+    do = torch.randn(q.shape, generator=torch.Generator("cpu").manual_seed(3)).half().to(gpu)
+    drop = (P, 777, 2**32 - 50_000)
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for keep in (True, False):
+        o = torch.full_like(q, float("nan"))
+        L = torch.empty((B, H, M), dtype=torch.float32, device=gpu)
+        a = _native.make_args(q, k, v, o, True, D ** -0.5, drop)
+        kbuf = None
+        if keep:
+            kptr, kbytes, kbuf = _common.workspace(_native.VARIANT_KEEP_BITS, a, 0, gpu)
+            assert kbytes > 0
+            a.keep_bits = kptr
+        wptr, wbytes, ws = _common.workspace(_native.VARIANT_ATTENTION_FORWARD, a, 0, gpu)
+        rc = lib.fas_attention_forward(ctypes.byref(a), L.data_ptr(), _native.strides3(L),
+                                       wptr, wbytes, stream)
+        _native.check(lib, rc, "fas_attention_forward")
+        grads = [torch.full_like(t, float("nan")) for t in (q, k, v)]
+        b = _native.make_args(q, k, v, o, True, D ** -0.5, drop, a.keep_bits)
+        wptr, wbytes, ws2 = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, b, 0, gpu)
+        rc = lib.fas_attention_backward(ctypes.byref(b), do.data_ptr(), _native.strides4(do),
+                                        L.data_ptr(), _native.strides3(L),
+                                        *(x for g in grads for x in (g.data_ptr(),
+                                                                     _native.strides4(g))),
+                                        wptr, wbytes, stream)
+        _native.check(lib, rc, "fas_attention_backward")
+        torch.cuda.synchronize()
+        outs.append((o, *grads))
+        del kbuf, ws, ws2
+    for name, x, y in zip(("o", "dq", "dk", "dv"), *outs):
+        assert not torch.isnan(x).any(), name
+        assert torch.equal(x, y), name

@@ -40,7 +40,24 @@ def header_functions():
 
 
 def test_library_loads_with_abi_version(lib):
-    assert lib.fas_abi_version() == _native.ABI_VERSION == 6
+    assert lib.fas_abi_version() == _native.ABI_VERSION == 7
+    m = re.search(r"#define FAS_ABI_VERSION (\d+)", open(HEADER).read())
+    assert m and int(m.group(1)) == _native.ABI_VERSION
+
+
+def test_keep_bits_size(lib):
+    """FAS_VARIANT_KEEP_BITS sizes the caller's keep-bit buffer: with dropout,
+    B*Hq*(ceil(M/32)*N + Mpad*ceil(N/32))*4 bytes in two 256-byte-aligned
+    parts; 0 without dropout."""
+    q = torch.empty(2, 3, 100, 64, dtype=torch.float16)
+    k = torch.empty(2, 3, 70, 64, dtype=torch.float16)
+    a = _native.make_args(q, k, k, q, True, 0.125, (0.1, 1, 0))
+    keys = 2 * 3 * 4 * 70 * 4                   # ceil(100/32) = 4 row words per key
+    rows = 2 * 3 * 128 * 3 * 4                  # Mpad 128, ceil(70/32) = 3 key words
+    al = lambda x: (x + 255) // 256 * 256
+    assert lib.fas_workspace_bytes(_native.VARIANT_KEEP_BITS, ctypes.byref(a), 0) == al(keys) + al(rows)
+    b = _native.make_args(q, k, k, q, True, 0.125)
+    assert lib.fas_workspace_bytes(_native.VARIANT_KEEP_BITS, ctypes.byref(b), 0) == 0
 
 
 def test_exports_match_header(lib):
