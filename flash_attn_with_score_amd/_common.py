@@ -118,17 +118,20 @@ def call(fn_name: str, q: torch.Tensor, *args) -> None:
     _native.check(lib, rc, fn_name)
 
 
-def workspace(variant: int, args, split: int, device) -> tuple[int, int, torch.Tensor | None]:
+def workspace(variant: int, args, split: int, device,
+              limit: int | None = None) -> tuple[int, int, torch.Tensor | None]:
     """Allocates the device workspace an entry point needs (torch caching
-    allocator, 256-byte aligned) and returns (pointer, bytes, tensor)."""
+    allocator, 256-byte aligned) and returns (pointer, bytes, tensor); with
+    `limit`, a workspace larger than that is not allocated (pointer 0, no
+    tensor) and the caller takes its route without it."""
     import ctypes
 
     lib = _native.load()
     nbytes = lib.fas_workspace_bytes(variant, ctypes.byref(args), int(split))
     if nbytes == ctypes.c_size_t(-1).value:
         raise RuntimeError(f"fas_workspace_bytes: {_native.last_error(lib) or 'invalid request'}")
-    if nbytes == 0:
-        return 0, 0, None
+    if nbytes == 0 or (limit is not None and nbytes > limit):
+        return 0, nbytes, None
     buf = torch.empty(nbytes + 256, dtype=torch.uint8, device=device)
     ptr = buf.data_ptr()
     ptr += (-ptr) % 256

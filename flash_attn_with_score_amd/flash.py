@@ -13,12 +13,19 @@ kernels for small grids and gives the same O and L.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import torch
 
 from . import _common, _native
 
 __all__ = ["attention", "FlashAttention"]
+
+# Largest keep-bit buffer (bytes) a forward with dropout holds for its
+# backward pass, about B*Hq*M*N/4; past it the backward evaluates the random
+# stream again, as the reference does.  FAS_KEEP_BITS_MAX_BYTES overrides it
+# (0 turns the buffer off).
+KEEP_BITS_MAX_BYTES = int(os.environ.get("FAS_KEEP_BITS_MAX_BYTES", 512 << 20))
 
 
 def _check_inputs(q, k, v):
@@ -40,7 +47,8 @@ def _forward(q, k, v, causal, sm_scale, want_total, dropout_p, keep=False):
     args = _native.make_args(p.q, p.k, p.v, o, causal, p.sm_scale, drop)
     kept = (0, None)
     if keep and drop is not None:
-        kptr, _, kbuf = _common.workspace(_native.VARIANT_KEEP_BITS, args, 0, q.device)
+        kptr, _, kbuf = _common.workspace(_native.VARIANT_KEEP_BITS, args, 0, q.device,
+                                          limit=KEEP_BITS_MAX_BYTES)
         if kbuf is not None:
             args.keep_bits = kptr
             kept = (kptr, kbuf)
@@ -66,9 +74,10 @@ class FlashAttention(torch.autograd.Function):
         _check_inputs(q, k, v)
         _common.check_device_inputs(q, k, v, dropout_p)
         # With dropout the forward keeps the mask's bits (B*Hq*M*N/8 bytes in
-        # two layouts, ~N*M/4 bytes per head) so that the backward reads the
-        # mask instead of evaluating the random stream again; the reference
-        # regenerates it (flash.py:653-659), with the same result.
+        # two layouts, ~N*M/4 bytes per head, up to KEEP_BITS_MAX_BYTES) so
+        # that the backward reads the mask instead of evaluating the random
+        # stream again; the reference regenerates it (flash.py:653-659), with
+        # the same result.
         need_grad = any(ctx.needs_input_grad[:3])
         p, o, L, tot, drop, kept = _forward(q, k, v, causal, sm_scale, return_total_attention,
                                             dropout_p, keep=need_grad)

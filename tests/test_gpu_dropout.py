@@ -263,3 +263,25 @@ def test_attention_keep_bits_match_philox(shape, gpu):
     for name, x, y in zip(("o", "dq", "dk", "dv"), *outs):
         assert not torch.isnan(x).any(), name
         assert torch.equal(x, y), name
+
+
+def test_attention_keep_bits_cap(monkeypatch, gpu):
+    """Past KEEP_BITS_MAX_BYTES attention()'s forward keeps no mask bits and
+    its backward evaluates the random stream again: O, dq, dk and dv are the
+    same bits either way."""
+    from flash_attn_with_score_amd import flash
+
+    B, H, Hk, M, N, D = 1, 4, 2, 200, 264, 64
+    print(f"[case] attention keep-bit cap B{B}H{H}K{Hk}M{M}N{N}D{D}", flush=True)
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=torch.bfloat16, seed=15, device=gpu)
+    do = torch.randn(q.shape, generator=torch.Generator("cpu").manual_seed(4)).bfloat16().to(gpu)
+    outs = []
+    for cap in (flash.KEEP_BITS_MAX_BYTES, 0):
+        monkeypatch.setattr(flash, "KEEP_BITS_MAX_BYTES", cap)
+        _set_state(gpu, 4242, 2**32 - 30_000)
+        qg, kg, vg = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        o = fas.attention(qg, kg, vg, causal=True, dropout_p=P)
+        outs.append((o, *torch.autograd.grad(o, (qg, kg, vg), do)))
+    torch.cuda.synchronize()
+    for name, x, y in zip(("o", "dq", "dk", "dv"), *outs):
+        assert torch.equal(x, y), name
