@@ -58,6 +58,10 @@ WORKLOADS = {
     "cross_qk": ("attention_cross_token_qk_sum", True, "mfma", 4),
     "cross_softmax": ("attention_cross_token_softmax_sum", True, "mfma", None),
     "cross_softmax_buffered": ("attention_cross_token_softmax_sum_buffered", True, "hbm", None),
+    # attention()'s forward pass (flash.py:32-169) with inputs that need
+    # gradients, as in training: O and L, plus the dropout keep bits the
+    # backward reads when dropout is on.
+    "attention_fwd": ("attention", False, "mfma", 4),
     # attention()'s backward pass alone (flash.py:172-261), FA2 convention:
     # 2.5x the forward's 4*B*H*D*P.
     "attention_bwd": ("attention", False, "mfma", 10),
@@ -98,7 +102,8 @@ def work(name: str, B, H, Hk, M, N, D, causal, split, elem=2):
         # reads q, k; writes the full score matrix
         return (fac * B * H * M * N * D,
                 elem * (B * H * M * D + B * Hk * N * D + B * H * M * N))
-    if name == "row_sum":
+    if name in ("row_sum", "attention_fwd"):
+        # + the (B, H, M) fp32 row sums / log-normalizer
         return 4 * B * H * D * P, qkvo + 4 * B * H * M
     if name in ("col_sum", "col_sum_sequential", "col_softmax"):
         return fac * B * H * D * P, qkvo + 4 * B * Hk * N
@@ -199,6 +204,11 @@ def synthetic_qkv(B, Hq, Hk, M, N, D, dtype, scale, device):
 
 
 def make_call(fas, name, q, k, v, causal, split, dropout_p=0.0):
+    if name == "attention_fwd":
+        # Each call builds the autograd graph (and, with dropout, the keep
+        # bits) and drops it with its output.
+        qg, kg, vg = (t.detach().requires_grad_(True) for t in (q, k, v))
+        return lambda: fas.attention(qg, kg, vg, causal=causal, dropout_p=dropout_p)
     if name == "attention_bwd":
         # One forward outside the timed calls; each call is one backward pass
         # through the autograd graph (dq, dk, dv).
@@ -386,7 +396,7 @@ def main() -> int:
 
     del q, k, v
     torch.cuda.synchronize()
-    if args.cpu_budget > 0 and args.workload not in ("attention_bwd", "scores_only"):
+    if args.cpu_budget > 0 and args.workload not in ("attention_fwd", "attention_bwd", "scores_only"):
         line["cpu_baseline"] = cpu_baseline(args.workload, B, H, Hk, M, N, D, causal, split,
                                             dtype, args.cpu_budget, args.input_scale)
     else:

@@ -286,11 +286,13 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
               keep[r] = dropout_keep(p.drop, idx);
             }
           }
+          f32x16 nd;  // -delta of row acc_row(r, g)
+          load8(nd, &xlds[stage][32 * qb + 8 * g], 0, 0);
+          load8(nd, &xlds[stage][32 * qb + 16 + 8 * g], 0, 1);
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float nd = xlds[stage][32 * qb + acc_row(r, g)];  // -delta
             s[r] = keep[r] ? pr[r] : 0.f;
-            dp[r] = pr[r] * ((keep[r] ? p.drop.scale * dp[r] : 0.f) + nd);
+            dp[r] = pr[r] * ((keep[r] ? p.drop.scale * dp[r] : 0.f) + nd[r]);
           }
           uint32_t word = 0;
           if (bits) {
