@@ -4,16 +4,24 @@
 
 namespace fas {
 
-template <class E, int D, bool DROP>
-static hipError_t bwd_drop_t(const BwdParams& p, hipStream_t s) {
+// Instances: DROP 0 without dropout; with dropout, the dK/dV kernel reads
+// the forward's keep words when given (2) or evaluates Philox (1), and the dQ
+// kernel reads keep bits when drop_bits holds them (2) or evaluates Philox (1).
+template <class E, int D>
+static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
   const int64_t bh = (int64_t)p.B * p.H;
   if (p.M > 0)
     hipLaunchKernelGGL((bwd_prep_kernel<E, D>), dim3((unsigned)(bh * p.nprep)), dim3(256), 0, s,
                        p);
   if (p.N > 0) {
     const int64_t rest = p.partial ? bh : (int64_t)p.B * p.Hk;
-    hipLaunchKernelGGL((bwd_dkdv_kernel<E, D, DROP>), dim3((unsigned)(rest * p.nkb)), dim3(256),
-                       0, s, p);
+    const dim3 grid((unsigned)(rest * p.nkb));
+    if (!p.dropout)
+      hipLaunchKernelGGL((bwd_dkdv_kernel<E, D, 0>), grid, dim3(256), 0, s, p);
+    else if (p.keep_keys)
+      hipLaunchKernelGGL((bwd_dkdv_kernel<E, D, 2>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((bwd_dkdv_kernel<E, D, 1>), grid, dim3(256), 0, s, p);
     if (p.partial) {
       const int64_t total = (int64_t)p.B * p.Hk * p.N * (D / 8);
       int64_t blocks = (total + 255) / 256;
@@ -22,15 +30,16 @@ static hipError_t bwd_drop_t(const BwdParams& p, hipStream_t s) {
                          p);
     }
   }
-  if (p.M > 0)
-    hipLaunchKernelGGL((bwd_dq_kernel<E, D, DROP>), dim3((unsigned)(bh * p.nrb)), dim3(256), 0, s,
-                       p);
+  if (p.M > 0) {
+    const dim3 grid((unsigned)(bh * p.nrb));
+    if (!p.dropout)
+      hipLaunchKernelGGL((bwd_dq_kernel<E, D, 0>), grid, dim3(256), 0, s, p);
+    else if (p.drop_bits)
+      hipLaunchKernelGGL((bwd_dq_kernel<E, D, 2>), grid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((bwd_dq_kernel<E, D, 1>), grid, dim3(256), 0, s, p);
+  }
   return hipGetLastError();
-}
-
-template <class E, int D>
-static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
-  return p.dropout ? bwd_drop_t<E, D, true>(p, s) : bwd_drop_t<E, D, false>(p, s);
 }
 
 hipError_t launch_bwd(const BwdParams& p, int dtype, int d, hipStream_t s) {

@@ -100,8 +100,10 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const BwdParams p) {
 
 // DROP: the forward's dropout mask Z (keep = 1) and r = 1/(1-p) enter as
 // dV = r sum_i (Z P)_ij dO_i and dS = P (r Z dP - delta) (flash.py:705-731);
-// the dP accumulator then starts at 0 and delta is added afterwards.
-template <class E, int D, bool DROP>
+// the dP accumulator then starts at 0 and delta is added afterwards.  DROP 1
+// evaluates Z (Philox) and, with drop_bits, stores it for the dQ kernel;
+// DROP 2 reads the forward's keep words (keep_keys) and has no Philox code.
+template <class E, int D, int DROP>
 __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
   constexpr int KS = D / 16;               // k-steps over the head dim
   constexpr int DB = D >= 32 ? D / 32 : 1;  // 32-dim blocks of dK^T / dV^T
@@ -165,8 +167,8 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
   // With the forward's keep words (keep_keys) the mask is read, not
   // evaluated, and nothing is stored for the dQ kernel; otherwise the
   // decisions are evaluated and, with drop_bits, stored for it.
-  const bool from_keys = DROP && p.keep_keys != nullptr;
-  const bool bits = DROP && p.drop_bits != nullptr && !from_keys;
+  constexpr bool from_keys = DROP == 2;
+  const bool bits = DROP == 1 && p.drop_bits != nullptr;
   const int r32 = (p.M + 31) >> 5;
   for (int hh = 0; hh < nheads && t0 < t1; ++hh) {
     const int h = h0 + hh;
@@ -182,15 +184,13 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
     // key0 + c, loaded with the tile's Q and dO.
     uint32_t kcur[2] = {0u, 0u}, knext[2] = {0u, 0u};
     auto fetch_keys = [&](int t, uint32_t (&w)[2]) __attribute__((always_inline)) {
-      if constexpr (DROP) {
-        if (from_keys) {
+      if constexpr (from_keys) {
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            const int key = key0 + c;
-            const uint32_t rw = (uint32_t)((t * TQ + 32 * qb) >> 5);
-            w[qb] = __builtin_amdgcn_raw_buffer_load_b32(
-                rkeys, key < p.N ? (rw * (uint32_t)p.N + (uint32_t)key) * 4u : kOffNoneBwd, 0, 0);
-          }
+        for (int qb = 0; qb < 2; ++qb) {
+          const int key = key0 + c;
+          const uint32_t rw = (uint32_t)((t * TQ + 32 * qb) >> 5);
+          w[qb] = __builtin_amdgcn_raw_buffer_load_b32(
+              rkeys, key < p.N ? (rw * (uint32_t)p.N + (uint32_t)key) * 4u : kOffNoneBwd, 0, 0);
         }
       }
     };
@@ -272,7 +272,7 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
           // interleave; the lane writes (inline assembly, which the compiler
           // does not move instructions across) follow in their own pass.
           bool keep[16];
-          if (from_keys) {
+          if constexpr (from_keys) {
             // Bit acc_row(r, g) = 16 (r / 8) + 8 g + r % 8 of the block's word.
             const uint32_t wb = kcur[qb] >> (8 * g);
 #pragma unroll
@@ -435,8 +435,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_reduce_kernel(const BwdParams p)
 
 // ---------------------------------------------------------------- dQ
 
-// DROP: dS = P (r Z dP - delta) as in the dK/dV kernel (flash.py:885-895).
-template <class E, int D, bool DROP>
+// DROP: dS = P (r Z dP - delta) as in the dK/dV kernel (flash.py:885-895),
+// Z by Philox (DROP 1) or from the keep bits in drop_bits (DROP 2).
+template <class E, int D, int DROP>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_dq_kernel(const BwdParams p) {
   constexpr int KS = D / 16;
   constexpr int DB = D >= 32 ? D / 32 : 1;
@@ -501,7 +502,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // Keep words of tile t (dropout with p.drop_bits): this row's keys
   // 64t .. 64t+31 and 64t+32 .. 64t+63, loaded with the tile's K and V.
-  const bool bits = DROP && p.drop_bits != nullptr;
+  constexpr bool bits = DROP == 2;
   __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
   if (bits)
     rbits = make_rsrc(p.drop_bits + (int64_t)bh * p.Mpad * p.n32,
@@ -584,7 +585,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         if (!full && acc_row(r, g) >= lim) pr[r] = 0.f;
       }
       if constexpr (DROP) {
-        if (bits) {
+        if constexpr (bits) {
           // The dK/dV kernel's keep bits: bit acc_row(r, g) of the word of
           // this row and sub-block.
           const uint32_t wb = wcur[kb2] >> (8 * g);
