@@ -465,12 +465,15 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
       off += align256((size_t)pr.B * pr.H * pr.N * 2 * pr.D * 4);
     }
     // With dropout the dK/dV kernel stores its keep decisions (one bit per
-    // pair) for the dQ kernel, when a head's words stay below 2 GiB.
+    // pair) for the dQ kernel, when a head's words stay below 2 GiB and the
+    // caller's workspace has room for them (fas_workspace_bytes includes
+    // them); otherwise the dQ kernel evaluates the Philox stream again.
     const size_t head_bytes = (size_t)bwd_mpad(pr) * ((pr.N + 31) / 32) * 4;
-    if (pr.dropout && !pr.keep && head_bytes < ((size_t)1 << 31)) {
+    const size_t bits = align256((size_t)pr.B * pr.H * head_bytes);
+    if (pr.dropout && !pr.keep && head_bytes < ((size_t)1 << 31) && off + bits <= budget) {
       w.has_bits = true;
       w.bits = off;
-      off += align256((size_t)pr.B * pr.H * head_bytes);
+      off += bits;
     }
   }
   if (raw) {
@@ -1001,7 +1004,7 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
     if ((rc = check_tensor(fn, "dk", dk, kst, pr.N, pr.D))) return rc;
     if ((rc = check_tensor(fn, "dv", dv, vst, pr.N, pr.D))) return rc;
   }
-  const Workspace w = layout(FAS_VARIANT_ATTENTION_BACKWARD, pr, 0);
+  const Workspace w = layout(FAS_VARIANT_ATTENTION_BACKWARD, pr, 0, ws_bytes);
   if ((rc = check_workspace(fn, w, ws, ws_bytes))) return rc;
   KeepLayout kl;
   if ((rc = check_keep(fn, a, pr, &kl))) return rc;

@@ -253,7 +253,11 @@ int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t 
  * dout is dL/dO (shaped like out).  Writes dq (like q) and dk, dv
  * (B, Hk, N, D) in the input dtype, dk and dv summed over the Hq/Hk query
  * heads of each KV head.  Needs fas_workspace_bytes(
- * FAS_VARIANT_ATTENTION_BACKWARD, a, 0) bytes of workspace. */
+ * FAS_VARIANT_ATTENTION_BACKWARD, a, 0) bytes of workspace.  With dropout
+ * and no keep_bits that size includes B*Hq*Mpad*ceil(N/32)*4 bytes (256-byte
+ * aligned, Mpad = M rounded up to 128) of keep bits passed from the dK/dV
+ * kernel to the dQ kernel; a workspace short of them (at least the rest)
+ * makes both kernels evaluate the random stream, with the same result. */
 int fas_attention_backward(const fas_attn_args* a, const void* dout,
                            const int64_t dout_stride[4], const float* lse,
                            const int64_t lse_stride[3], void* dq, const int64_t dq_stride[4],

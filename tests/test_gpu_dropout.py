@@ -285,3 +285,53 @@ def test_attention_keep_bits_cap(monkeypatch, gpu):
     torch.cuda.synchronize()
     for name, x, y in zip(("o", "dq", "dk", "dv"), *outs):
         assert torch.equal(x, y), name
+
+
+def test_attention_backward_without_bit_workspace(gpu):
+    """fas_attention_backward with dropout and no keep_bits: given a
+    workspace short of the keep-bit part, the dQ kernel evaluates the Philox
+    stream instead of reading the dK/dV kernel's bits; dq, dk and dv are the
+    same bits either way (64-bit offset carrying into counter word 1)."""
+    from flash_attn_with_score_amd import _common, _native
+
+    B, H, Hk, M, N, D = 2, 4, 2, 150, 300, 64
+    print(f"[case] backward without keep-bit workspace B{B}H{H}K{Hk}M{M}N{N}D{D}", flush=True)
+    lib = _native.load()
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=torch.float16, seed=16, device=gpu)
+    do = torch.randn(q.shape, generator=torch.Generator("cpu").manual_seed(5)).half().to(gpu)
+    drop = (P, 99, 2**32 - 40_000)
+    stream = torch.cuda.current_stream().cuda_stream
+    o = torch.empty_like(q)
+    L = torch.empty((B, H, M), dtype=torch.float32, device=gpu)
+    a = _native.make_args(q, k, v, o, True, D ** -0.5, drop)
+    wptr, wbytes, ws = _common.workspace(_native.VARIANT_ATTENTION_FORWARD, a, 0, gpu)
+    _native.check(lib, lib.fas_attention_forward(ctypes.byref(a), L.data_ptr(),
+                                                 _native.strides3(L), wptr, wbytes, stream),
+                  "fas_attention_forward")
+    full = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0)
+    mpad = (M + 127) // 128 * 128
+    bits = (B * H * mpad * ((N + 31) // 32) * 4 + 255) // 256 * 256
+    outs = []
+    for nbytes in (full, full - bits):
+        buf = torch.empty(full + 256, dtype=torch.uint8, device=gpu)
+        ptr = buf.data_ptr() + (-buf.data_ptr()) % 256
+        grads = [torch.full_like(t, float("nan")) for t in (q, k, v)]
+        rc = lib.fas_attention_backward(ctypes.byref(a), do.data_ptr(), _native.strides4(do),
+                                        L.data_ptr(), _native.strides3(L),
+                                        *(x for g in grads for x in (g.data_ptr(),
+                                                                     _native.strides4(g))),
+                                        ptr, nbytes, stream)
+        _native.check(lib, rc, "fas_attention_backward")
+        torch.cuda.synchronize()
+        outs.append(grads)
+        del buf
+    for name, x, y in zip(("dq", "dk", "dv"), *outs):
+        assert not torch.isnan(x).any(), name
+        assert torch.equal(x, y), name
+    # Short of the base part the call is refused.
+    rc = lib.fas_attention_backward(ctypes.byref(a), do.data_ptr(), _native.strides4(do),
+                                    L.data_ptr(), _native.strides3(L),
+                                    *(x for g in outs[0] for x in (g.data_ptr(),
+                                                                   _native.strides4(g))),
+                                    wptr or 0, 256, stream)
+    assert rc == _native.FAS_ERR_WORKSPACE
