@@ -264,8 +264,14 @@ void colsm64_kernel(const ColsmParams p) {
                 if (!dropout_keep(p.drop, idx)) s[j][r] = 0.f;
               }
               if constexpr (DROP == 2) {
-                // Bit acc_row(r, g) = 16 (r / 8) + 8 g + r % 8 of the block's word.
-                if (!((bcur[2 * qb + j] >> (8 * g + 16 * (r >> 3) + (r & 7))) & 1u)) s[j][r] = 0.f;
+                // Bit acc_row(r, g) = 16 (r / 8) + 8 g + r % 8 of the block's
+                // word, sign-extended to a mask (0 or all ones) for the weight.
+                // (Through a float local: bit_cast of a vector element itself
+                // read element 0 in this compiler.)
+                const int m = __builtin_amdgcn_sbfe((int)(bcur[2 * qb + j] >> (8 * g)),
+                                                    16 * (r >> 3) + (r & 7), 1);
+                const float w = s[j][r];
+                s[j][r] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, w) & (uint32_t)m);
               }
             }
 #pragma unroll
