@@ -228,8 +228,10 @@ __device__ __forceinline__ void sched_score_tile() {
 // PACK: GQA packing (p.pack query heads per workgroup, per-lane heads and
 // positions); without it the workgroup's rows are one head's and every
 // per-lane head offset folds away at compile time.
+// Two waves per SIMD, except for the 4-wave score writer, whose LDS (one
+// workgroup per CU) allows one.
 template <class E, int D, int MODE, int NW, bool DROP, bool PACK>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 1 : 2, 2)))
 void fwd_kernel(const FwdParams p) {
   static_assert(MODE != kFwdScores || NW == 8 || NW == 4, "the score writer uses 4 or 8 waves");
   constexpr int NH = NW / 2;  // score writer: loader waves [0, NH), storer waves [NH, NW)

@@ -74,6 +74,11 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
 // forward pass stored (one word per key and 32-row block, prefetched with
 // the next step's Q rows).
 // The sign of a negative sm_scale is applied to K once per block.
+// The Philox instances (DROP 1, used only when the keep bits do not fit) are
+// too large for the compiler to unroll the two-block loop below; it stays a
+// loop there, and the warning saying so is silenced.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Wpass-failed"
 template <class E, int D, bool LN, int DROP>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void colsm64_kernel(const ColsmParams p) {
@@ -317,6 +322,7 @@ void colsm64_kernel(const ColsmParams p) {
     __syncthreads();
   }
 }
+#pragma clang diagnostic pop
 
 // Buffered source: pass 1 left the raw fp32 scores of the region (rows >=
 // split, keys < split; masked entries -inf) in p.region.  A workgroup of 4
