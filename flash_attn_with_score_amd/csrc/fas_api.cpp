@@ -303,6 +303,9 @@ struct Workspace {
   size_t bits = 0;                                              // dropout keep bits
   bool has_bits = false;
   size_t nl = 0, delta = 0;                                     // backward row values
+  size_t ds = 0;                                                // backward dS blocks
+  int64_t ds_head = 0;
+  bool has_ds = false;
   size_t so = 0, sm = 0, sl = 0, sr = 0;                        // key-split partials
   bool has_lse = false, has_part = false, has_bsum = false, has_region = false;
   bool has_split = false;
@@ -370,6 +373,22 @@ int64_t bwd_nkb(const Problem& pr) { return ((int64_t)pr.N + fas::kBwdBlock - 1)
 bool bwd_partial(const Problem& pr) {
   return pr.G > 1 && (int64_t)pr.B * pr.Hk * bwd_nkb(pr) < 256;
 }
+// The backward's stored dS (BwdParams.ds): 32-row block r sees 32-key blocks
+// [0, clamp(r + a, 0, ceil(N/32))): a = floor((N - M + 31) / 32) + 1 under the
+// causal mask (block (r, j) holds a visible pair iff (N - M) + 32 r + 31 >=
+// 32 j), every block without it.
+int64_t bwd_ds_a(const Problem& pr) {
+  const int64_t n32 = ((int64_t)pr.N + 31) / 32;
+  if (!pr.causal) return n32;
+  const int64_t x = (int64_t)pr.N - pr.M + 31;
+  return (x >= 0 ? x / 32 : -((-x + 31) / 32)) + 1;
+}
+int64_t bwd_ds_head(const Problem& pr) {
+  return fas::ds_block_start(bwd_mpad(pr) / 32, bwd_ds_a(pr), ((int64_t)pr.N + 31) / 32);
+}
+// Largest dS workspace the backward takes (all heads); past it, and when one
+// head's blocks reach 2 GiB, the dQ kernel recomputes S and dP instead.
+constexpr size_t kBwdDsMaxBytes = (size_t)16 << 30;
 
 // The caller's keep-bit buffer (fas_attn_args.keep_bits) of attention's
 // forward and backward: key-major words for the dK/dV kernel (word
@@ -464,13 +483,28 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
       w.part = off;
       off += align256((size_t)pr.B * pr.H * pr.N * 2 * pr.D * 4);
     }
-    // With dropout the dK/dV kernel stores its keep decisions (one bit per
-    // pair) for the dQ kernel, when a head's words stay below 2 GiB and the
-    // caller's workspace has room for them (fas_workspace_bytes includes
-    // them); otherwise the dQ kernel evaluates the Philox stream again.
+    // dS for the dQ kernel (2 bytes per visible pair, in 32 x 32 blocks),
+    // when a head's blocks stay below 2 GiB, all of them within
+    // kBwdDsMaxBytes and the caller's workspace has room for them
+    // (fas_workspace_bytes includes them unless asked with split != 0).
+    const int64_t ds_head = bwd_ds_head(pr);
+    const size_t ds_bytes = align256((size_t)pr.B * pr.H * (size_t)ds_head * 2048);
+    if (split == 0 && pr.M > 0 && pr.N > 0 && ds_head * 2048 < ((int64_t)1 << 31) &&
+        ds_bytes <= kBwdDsMaxBytes && off + ds_bytes <= budget) {
+      w.has_ds = true;
+      w.ds = off;
+      w.ds_head = ds_head;
+      off += ds_bytes;
+    }
+    // Without stored dS, with dropout, the dK/dV kernel stores its keep
+    // decisions (one bit per pair) for the dQ kernel, when a head's words
+    // stay below 2 GiB and the caller's workspace has room for them
+    // (fas_workspace_bytes includes them); otherwise the dQ kernel evaluates
+    // the Philox stream again.
     const size_t head_bytes = (size_t)bwd_mpad(pr) * ((pr.N + 31) / 32) * 4;
     const size_t bits = align256((size_t)pr.B * pr.H * head_bytes);
-    if (pr.dropout && !pr.keep && head_bytes < ((size_t)1 << 31) && off + bits <= budget) {
+    if (!w.has_ds && pr.dropout && !pr.keep && head_bytes < ((size_t)1 << 31) &&
+        off + bits <= budget) {
       w.has_bits = true;
       w.bits = off;
       off += bits;
@@ -714,6 +748,8 @@ size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM ||
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED;
   if (has_split && !(split > 0 && split <= pr.N)) return (size_t)-1;
+  // The backward: split != 0 asks for the size without the stored dS.
+  const bool bwd = variant == FAS_VARIANT_ATTENTION_BACKWARD;
   // The key-split plan depends on the GQA packing, which a launch picks
   // from the strides; the size covers both choices, so a query made with
   // placeholder strides still suffices.
@@ -721,7 +757,7 @@ size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
   for (int pk : {1, pr.G}) {
     Problem q = pr;
     q.pack = pk;
-    total = std::max(total, layout(variant, q, has_split ? split : 0).total);
+    total = std::max(total, layout(variant, q, has_split || bwd ? split : 0).total);
   }
   return total;
 }
@@ -1051,6 +1087,11 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   p.partial = bwd_partial(pr) ? 1 : 0;
   p.n32 = (pr.N + 31) / 32;
   if (w.has_bits) p.drop_bits = at<uint32_t>(ws, w.bits);
+  if (w.has_ds) {
+    p.ds = at<uint16_t>(ws, w.ds);
+    p.ds_head = w.ds_head;
+    p.ds_a = (int)bwd_ds_a(pr);
+  }
   if (pr.keep) {
     // The forward's bits: dK/dV reads the key-major words, dQ the row blocks.
     p.keep_keys = at<uint32_t>(a->keep_bits, kl.keys);

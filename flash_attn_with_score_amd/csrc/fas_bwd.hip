@@ -5,8 +5,10 @@
 namespace fas {
 
 // Instances: DROP 0 without dropout; with dropout, the dK/dV kernel reads
-// the forward's keep words when given (2) or evaluates Philox (1), and the dQ
-// kernel reads keep bits when drop_bits holds them (2) or evaluates Philox (1).
+// the forward's keep words when given (2) or evaluates Philox (1).  dQ comes
+// from the stored dS blocks when p.ds is set (bwd_dq_ds_kernel, no dropout
+// instances: dS carries the mask); otherwise bwd_dq_kernel recomputes S and
+// dP, reading keep bits when drop_bits holds them (2) or evaluating Philox (1).
 template <class E, int D>
 static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
   const int64_t bh = (int64_t)p.B * p.H;
@@ -32,7 +34,9 @@ static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
   }
   if (p.M > 0) {
     const dim3 grid((unsigned)(bh * p.nrb));
-    if (!p.dropout)
+    if (p.ds)
+      hipLaunchKernelGGL((bwd_dq_ds_kernel<E, D>), grid, dim3(256), 0, s, p);
+    else if (!p.dropout)
       hipLaunchKernelGGL((bwd_dq_kernel<E, D, 0>), grid, dim3(256), 0, s, p);
     else if (p.drop_bits)
       hipLaunchKernelGGL((bwd_dq_kernel<E, D, 2>), grid, dim3(256), 0, s, p);

@@ -196,6 +196,15 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
     };
     const i32x4 wq = make_rsrc_words(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
     const i32x4 wg = make_rsrc_words(p.dout + b * p.sg0 + h * p.sg1, p.g_bytes);
+    // dS blocks for bwd_dq_ds_kernel (p.ds): block (r0/32, key0/32) of this
+    // head, lane l's 16 bytes of the first half (rows acc_row(0..7, g)) at
+    // 16 l, of the second half (rows acc_row(8..15, g)) at 1024 + 16 l.
+    // Non-temporal: the dS stream (about B*H*M*N bytes) would otherwise
+    // evict the Q and dO tiles every key block re-reads from L2.
+    const bool store_ds = p.ds != nullptr && key0 < p.N;
+    const __amdgpu_buffer_rsrc_t rds =
+        make_rsrc(p.ds + (store_ds ? bh * p.ds_head * 1024 : 0),
+                  store_ds ? (uint32_t)(p.ds_head * 2048) : 0u);
     const float* nlg = p.nl + bh * p.Mpad;
     const float* xg = p.delta + bh * p.Mpad;
     float nst = 0.f, xst = 0.f;
@@ -323,6 +332,12 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
         }
         const u32x4 pb0 = pack_b<E>(s, 0), pb1 = pack_b<E>(s, 1);
         const u32x4 sb0 = pack_b<E>(dp, 0), sb1 = pack_b<E>(dp, 1);
+        if (store_ds) {
+          const uint32_t blk =
+              (uint32_t)(ds_block_start32(r0 >> 5, p.ds_a, p.n32) + (key0 >> 5)) * 2048u;
+          buf_store16_nt(sb0, rds, blk + 16u * (uint32_t)lane);
+          buf_store16_nt(sb1, rds, blk + 1024u + 16u * (uint32_t)lane);
+        }
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
           dv[db] = E::mma(lds_vt_operand<D>(gt, db, 2 * qb, lane), pb0, dv[db]);
@@ -644,6 +659,153 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 
   // Lane (c, g), register r of block db: row qrow, head dim 32db + acc_row(r, g).
+  if (qrow >= p.M) return;
+  uint16_t* dqr = p.dq + b * p.sdq0 + h * p.sdq1 + (int64_t)qrow * p.sdq2;
+#pragma unroll
+  for (int db = 0; db < DB; ++db)
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const int d0 = 32 * db + 16 * hf + 8 * g;
+      if (d0 < D) {
+        const f32x16 x = dq[db] * p.scale_signed;
+        *reinterpret_cast<u32x4*>(dqr + d0) = pack_b<E>(x, hf);
+      }
+    }
+}
+
+// dQ from the dS blocks the dK/dV kernel stored (p.ds): query-block outer, a
+// wave owns 32 rows and streams 64-key tiles; per tile the workgroup's K rows
+// and each wave's two dS blocks arrive in LDS by DMA, and
+//   dQ^T += K^T dS^T
+// takes both operands from LDS with the transposing read.  The dS blocks
+// are stored key-major (lane = key, eight rows per 16 bytes), so the DMA
+// gathers them into a swizzled [64 keys][32 rows] tile, whose transposing
+// read yields rows on lanes and eight consecutive keys per lane, the B
+// operand; lane c then holds row perm_row(c) of the wave.  Blocks a causal
+// mask hides were never stored and are not read.  No recomputation of S and
+// dP, no dropout (dS already carries it), and the same dS values as dK.
+//
+// The kernel is bound by the dS stream from HBM, so dS runs two tiles ahead
+// (three LDS stages) and K, mostly an L2 hit, one tile ahead (two stages):
+// 80 KiB of LDS, two workgroups per CU.  Every wave issues exactly four dS
+// DMAs per tile (blocks outside the visible range read from an offset past
+// the buffer: zeros, no memory traffic), after the tile's K DMAs, so
+// "vmcnt <= 4" at the end of a step means everything but the newest dS tile
+// has landed (vector loads complete in issue order).
+template <class E, int D>
+__global__ __launch_bounds__(256) void bwd_dq_ds_kernel(const BwdParams p) {
+  constexpr int DB = D >= 32 ? D / 32 : 1;
+  constexpr int NW = 4;
+  constexpr int BM = 32 * NW;     // query rows per workgroup
+  constexpr int BN = 64;          // keys per tile
+  constexpr int TILE = BN * D;
+  constexpr int STILE = BN * 32;  // a wave's dS^T tile
+
+  __shared__ __attribute__((aligned(16))) uint16_t klds[2][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t slds[3][NW][STILE];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, c = lane & 31, g = lane >> 5;
+  // Workgroup i runs on XCD i % 8: each XCD takes a contiguous run of
+  // (head, row block) pairs, head-major, so the workgroups running at once
+  // on one XCD share a head or two and their K rows stay in its L2.
+  const int total = p.B * p.H * p.nrb;
+  int bid = blockIdx.x;
+  if (total % 8 == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  const int bh = bid / p.nrb;
+  int rb = bid % p.nrb;
+  if (p.causal) rb = p.nrb - 1 - rb;  // longest row blocks first
+  const int b = bh / p.H, h = bh % p.H, hk = h / p.G;
+  const int row0 = rb * BM, wrow0 = row0 + 32 * wave;
+
+  // Key tiles of the workgroup; this wave's visible 32-key blocks [0, wblk).
+  const int hi = p.causal ? min(p.N, max(0, p.causal_off + row0 + BM)) : p.N;
+  const int ntiles = (hi + BN - 1) / BN;
+  const int whi = wrow0 >= p.M ? 0
+                  : p.causal ? min(p.N, max(0, p.causal_off + wrow0 + 32))
+                             : p.N;
+  const int wblk = (whi + 31) >> 5;
+  const uint32_t sblk =
+      wblk > 0 ? (uint32_t)ds_block_start32(wrow0 >> 5, p.ds_a, p.n32) * 2048u : 0u;
+
+  const i32x4 wk = make_rsrc_words(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
+  const i32x4 wd = make_rsrc_words(p.ds + (int64_t)bh * p.ds_head * 1024,
+                                    (uint32_t)(p.ds_head * 2048));
+  const uint32_t k_base = lds_addr(&klds[0][0]);
+  const uint32_t s_base = lds_addr(&slds[0][wave][0]);
+  // DMA lane l of step i fills tile key 16 i + l / 4, physical chunk l % 4,
+  // i.e. rows 8 ch .. 8 ch + 7 with ch = (l % 4) ^ swz<32>(key): half ch / 2
+  // of the stored block, lane (key % 32) + 32 (ch % 2).
+  uint32_t goff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = 16 * i + (lane >> 2);
+    const int ch = (lane & 3) ^ swz<32>(key);
+    goff[i] = (uint32_t)((key >> 5) * 2048 + (ch >> 1) * 1024 + ((key & 31) + 32 * (ch & 1)) * 16);
+  }
+  auto fetch_k = [&](int t) __attribute__((always_inline)) {
+    dma_tile<D, BN, NW>(wk, p.sk2, t * BN, k_base + (uint32_t)((t & 1) * TILE * 2), wave, lane);
+  };
+  auto fetch_s = [&](int t) __attribute__((always_inline)) {
+    const uint32_t lb = s_base + (uint32_t)((t % 3) * NW * STILE * 2);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool vis = 2 * t + (i >> 1) < wblk;
+      dma16_nt(wd, vis ? sblk + (uint32_t)(2 * t) * 2048u + goff[i] : kOffNoneBwd,
+               lb + 1024u * (uint32_t)i);
+    }
+  };
+  // Everything issued except the newest tile's four dS DMAs (if any).
+  auto wait_ahead = [&](bool ahead) __attribute__((always_inline)) {
+    if (ahead)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      vm_wait_all();
+  };
+
+  f32x16 dq[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) dq[db] = f32x16{};
+  const VtOff vto = vt_offsets<D>(lane);
+  const VtOff vts = vt_offsets<32>(lane);
+
+  if (ntiles > 0) {
+    fetch_k(0);
+    fetch_s(0);
+    if (ntiles > 1) fetch_s(1);
+    wait_ahead(ntiles > 1);
+    __syncthreads();
+  }
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) fetch_k(t + 1);
+    if (t + 2 < ntiles) fetch_s(t + 2);
+    const uint16_t* kt = klds[t & 1];
+    const uint16_t* st = slds[t % 3][wave];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; ++kb2) {
+      if (2 * t + kb2 < wblk) {
+        VtOff o = vto, os = vts;
+        opaque(o);
+        opaque(os);
+        const u32x4 sb0 = lds_vt_operand<32>(st, os, 0, 2 * kb2);
+        const u32x4 sb1 = lds_vt_operand<32>(st, os, 0, 2 * kb2 + 1);
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          dq[db] = E::mma(lds_vt_operand<D>(kt, o, db, 2 * kb2), sb0, dq[db]);
+          dq[db] = E::mma(lds_vt_operand<D>(kt, o, db, 2 * kb2 + 1), sb1, dq[db]);
+        }
+      }
+    }
+    if (t + 1 < ntiles) {
+      wait_ahead(t + 2 < ntiles);
+      __syncthreads();
+    }
+  }
+
+  // Lane (c, g), register r of block db: row wrow0 + perm_row(c), head dim
+  // 32db + acc_row(r, g).
+  const int qrow = wrow0 + perm_row(c);
   if (qrow >= p.M) return;
   uint16_t* dqr = p.dq + b * p.sdq0 + h * p.sdq1 + (int64_t)qrow * p.sdq2;
 #pragma unroll

@@ -198,7 +198,36 @@ struct BwdParams {
   // Philox and does not write drop_bits (which then holds the forward's
   // row blocks).
   const uint32_t* keep_keys;
+  // Optional: dS = P (dP - delta) in the input type, stored by the dK/dV
+  // kernel and read by bwd_dq_ds_kernel (dQ = s dS K, no recomputation).
+  // Per (b, h): ds_head blocks of 32 rows x 32 keys, 2 KiB each, only the
+  // blocks a causal mask leaves visible (ds_block_start); null: bwd_dq_kernel
+  // recomputes S and dP.
+  uint16_t* ds;
+  int64_t ds_head;       // blocks per (b, h); ds_head * 2048 < 2^31
+  int ds_a;              // visible 32-key blocks of 32-row block r: clamp(r + ds_a, 0, n32)
 };
+
+// First dS block of 32-row block r in its head's compact layout: the sum over
+// r' < r of clamp(r' + a, 0, n), the visible 32-key blocks of each earlier
+// row block (a = n for no mask).  Closed form: rows with r' + a <= 0 add
+// nothing, rows with r' + a >= n add n, the rows between an arithmetic run.
+__host__ __device__ inline int64_t ds_block_start(int64_t r, int64_t a, int64_t n) {
+  const int64_t lo = a < 0 ? -a : 0;
+  const int64_t hi = n - a > lo ? n - a : lo;
+  const int64_t r1 = r < lo ? lo : (r > hi ? hi : r);
+  const int64_t up = r > hi ? r - hi : 0;
+  return (r1 - lo) * (lo + r1 - 1 + 2 * a) / 2 + n * up;
+}
+// The same in 32-bit arithmetic, for heads whose blocks number below 2^20
+// (every term and partial sum then stays below 2^21).
+__host__ __device__ inline int ds_block_start32(int r, int a, int n) {
+  const int lo = a < 0 ? -a : 0;
+  const int hi = n - a > lo ? n - a : lo;
+  const int r1 = r < lo ? lo : (r > hi ? hi : r);
+  const int up = r > hi ? r - hi : 0;
+  return (r1 - lo) * (lo + r1 - 1 + 2 * a) / 2 + n * up;
+}
 
 }  // namespace fas
 

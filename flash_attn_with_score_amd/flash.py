@@ -6,7 +6,9 @@ natural-log normalizer L = m * sm_scale + ln(l) (flash.py:477-483); with
 return_total_attention the key-outer column pass sums the softmax weights per
 query head (total.py:9-48).  The backward pass (flash.py:172-261) runs three
 gfx950 kernels through fas_attention_backward: delta = rowsum(O * dO), the
-key-outer dK/dV kernel and the query-outer dQ kernel.  The reference's
+key-outer dK/dV kernel, which also stores dS when the workspace holds it, and
+the query-outer dQ kernel (dQ = dS K from the stored dS, or recomputing S and
+dP).  The reference's
 split-KV forward (flash.py:66-136) is a scheduling choice of its Triton
 kernels for small grids and gives the same O and L.
 """
@@ -26,6 +28,14 @@ __all__ = ["attention", "FlashAttention"]
 # stream again, as the reference does.  FAS_KEEP_BITS_MAX_BYTES overrides it
 # (0 turns the buffer off).
 KEEP_BITS_MAX_BYTES = int(os.environ.get("FAS_KEEP_BITS_MAX_BYTES", 512 << 20))
+
+# Largest workspace (bytes) the backward pass allocates.  The full size holds
+# dS in the input dtype for every visible (query, key) pair, about B*Hq*M*N
+# bytes causal and twice that without a mask (at most 16 GiB, a limit of the
+# library), which the dQ kernel reads instead of recomputing S and dP; past
+# this limit the backward takes the smaller workspace and recomputes.
+# FAS_BWD_WORKSPACE_MAX_BYTES overrides it (0: always recompute).
+BWD_WORKSPACE_MAX_BYTES = int(os.environ.get("FAS_BWD_WORKSPACE_MAX_BYTES", 16 << 30))
 
 
 def _check_inputs(q, k, v):
@@ -109,7 +119,11 @@ class FlashAttention(torch.autograd.Function):
         args = _native.make_args(q, k, v, o, ctx.causal, ctx.sm_scale, ctx.drop,
                                  ctx.keep_ptr if ctx.keep_buf is not None else 0)
         ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args, 0,
-                                                 q.device)
+                                                 q.device, limit=BWD_WORKSPACE_MAX_BYTES)
+        if ws is None and ws_bytes > 0:
+            # Over the limit: the workspace without the stored dS (split != 0).
+            ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args,
+                                                     1, q.device)
         _common.call("fas_attention_backward", q, ctypes.byref(args), do.data_ptr(),
                      _native.strides4(do), L.data_ptr(), _native.strides3(L), dq.data_ptr(),
                      _native.strides4(dq), dk.data_ptr(), _native.strides4(dk), dv.data_ptr(),

@@ -9,7 +9,7 @@ tolerance of the fp64 oracle gradients (oracle/naive.attention_reference).
 Shapes cover MHA and GQA in both dK/dV modes (whole group per workgroup, and
 per-head fp32 partials when that leaves too few workgroups), every head dim,
 non-divisible lengths, M < N, M > N (rows with no key) and a negative
-sm_scale.
+sm_scale, and both dQ routes (stored dS, recomputed S and dP).
 """
 from __future__ import annotations
 
@@ -83,6 +83,35 @@ def test_attention_forward_and_backward(case, dtype, gpu):
     assert_out_close(dq, ref["dq"], "dq")
     assert_out_close(dk, ref["dk"], "dk")
     assert_out_close(dv, ref["dv"], "dv")
+
+
+@pytest.mark.parametrize("case", CASES, ids=_label)
+def test_attention_backward_both_dq_routes(case, monkeypatch, gpu):
+    """The backward's two dQ routes: from the dS blocks the dK/dV kernel
+    stores (the default workspace) and, with the workspace limited below
+    them (FAS_BWD_WORKSPACE_MAX_BYTES), recomputing S and dP.  dk and dv come
+    from the same dK/dV kernel and are equal bit for bit; dq of each route
+    is within the output tolerance of the fp64 oracle."""
+    from flash_attn_with_score_amd import flash
+
+    B, Hq, Hk, M, N, D, causal, sm_scale = case
+    print(f"[case] attention dq routes {_label(case)}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=torch.float16, seed=9)
+    do = torch.randn(B, Hq, M, D, generator=torch.Generator("cpu").manual_seed(10)).half()
+    grads = []
+    for limit in (flash.BWD_WORKSPACE_MAX_BYTES, 0):
+        monkeypatch.setattr(flash, "BWD_WORKSPACE_MAX_BYTES", limit)
+        qd, kd, vd = (t.to(gpu).requires_grad_(True) for t in (q, k, v))
+        o = fas.attention(qd, kd, vd, causal=causal, sm_scale=sm_scale)
+        grads.append(torch.autograd.grad(o, (qd, kd, vd), do.to(gpu)))
+    torch.cuda.synchronize()
+    (dq0, dk0, dv0), (dq1, dk1, dv1) = grads
+    assert torch.equal(dk0, dk1) and torch.equal(dv0, dv1)
+    ref = naive.attention_reference(q, k, v, do, causal=causal, sm_scale=sm_scale)
+    assert_out_close(dq0, ref["dq"], "dq (stored dS)")
+    assert_out_close(dq1, ref["dq"], "dq (recomputed)")
+    assert_out_close(dk0, ref["dk"], "dk")
+    assert_out_close(dv0, ref["dv"], "dv")
 
 
 def test_attention_large_magnitude_inputs(gpu):

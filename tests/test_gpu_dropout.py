@@ -288,10 +288,13 @@ def test_attention_keep_bits_cap(monkeypatch, gpu):
 
 
 def test_attention_backward_without_bit_workspace(gpu):
-    """fas_attention_backward with dropout and no keep_bits: given a
-    workspace short of the keep-bit part, the dQ kernel evaluates the Philox
-    stream instead of reading the dK/dV kernel's bits; dq, dk and dv are the
-    same bits either way (64-bit offset carrying into counter word 1)."""
+    """fas_attention_backward with dropout and no keep_bits, on the route
+    that recomputes S and dP for dQ (a workspace without the stored dS):
+    given a workspace short of the keep-bit part as well, the dQ kernel
+    evaluates the Philox stream instead of reading the dK/dV kernel's bits;
+    dq, dk and dv are the same bits either way (64-bit offset carrying into
+    counter word 1).  The full workspace (stored dS, whose values carry the
+    mask) gives the same dk and dv bits and dq within the oracle tolerance."""
     from flash_attn_with_score_amd import _common, _native
 
     B, H, Hk, M, N, D = 2, 4, 2, 150, 300, 64
@@ -309,11 +312,15 @@ def test_attention_backward_without_bit_workspace(gpu):
                                                  _native.strides3(L), wptr, wbytes, stream),
                   "fas_attention_forward")
     full = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0)
+    nods = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 1)
     mpad = (M + 127) // 128 * 128
     bits = (B * H * mpad * ((N + 31) // 32) * 4 + 255) // 256 * 256
+    assert full > nods > bits
     outs = []
-    for nbytes in (full, full - bits):
-        buf = torch.empty(full + 256, dtype=torch.uint8, device=gpu)
+    for nbytes in (nods, nods - bits, full):
+        # All-ones bytes (NaN in fp16 and fp32): no kernel may read a
+        # workspace element it did not write.
+        buf = torch.full((full + 256,), 255, dtype=torch.uint8, device=gpu)
         ptr = buf.data_ptr() + (-buf.data_ptr()) % 256
         grads = [torch.full_like(t, float("nan")) for t in (q, k, v)]
         rc = lib.fas_attention_backward(ctypes.byref(a), do.data_ptr(), _native.strides4(do),
@@ -325,9 +332,16 @@ def test_attention_backward_without_bit_workspace(gpu):
         torch.cuda.synchronize()
         outs.append(grads)
         del buf
-    for name, x, y in zip(("dq", "dk", "dv"), *outs):
-        assert not torch.isnan(x).any(), name
+    for name, x, y, z in zip(("dq", "dk", "dv"), *outs):
+        assert not torch.isnan(x).any() and not torch.isnan(z).any(), name
         assert torch.equal(x, y), name
+        if name != "dq":
+            assert torch.equal(x, z), name
+    r = naive.attention_reference(q.cpu(), k.cpu(), v.cpu(), do.cpu(), causal=True,
+                                  dropout=drop)
+    for name, i in (("dq", 0), ("dk", 1), ("dv", 2)):
+        assert_out_close(outs[0][i], r[name], name)
+        assert_out_close(outs[2][i], r[name], name)
     # Short of the base part the call is refused.
     rc = lib.fas_attention_backward(ctypes.byref(a), do.data_ptr(), _native.strides4(do),
                                     L.data_ptr(), _native.strides3(L),

@@ -111,24 +111,55 @@ def test_workspace_sizes(lib):
         r256(B * 4 * M * 4)
 
 
+def _ds_blocks(M, N, causal):
+    """dS blocks (32 rows x 32 keys) the backward stores per head, counted one
+    by one: rows padded to whole 128-row blocks, and under the causal mask
+    only blocks holding a visible pair, (N - M) + i >= j for some row i and
+    key j of the block."""
+    mpad = (M + 127) // 128 * 128
+    n32 = (N + 31) // 32
+    return sum(1 for r in range(mpad // 32) for j in range(n32)
+               if not causal or (N - M) + 32 * r + 31 >= 32 * j)
+
+
 def test_attention_backward_workspace(lib):
     """Two (B*Hq, Mpad) fp32 row arrays, Mpad = M rounded up to 128, plus
     per-query-head fp32 dK|dV partials only when Hq > Hk and the KV-head
-    grid B*Hk*ceil(N/128) is below 256 workgroups."""
+    grid B*Hk*ceil(N/128) is below 256 workgroups, plus 2 KiB per stored dS
+    block, which a query with split != 0 leaves out."""
     def r256(x):
         return (x + 255) // 256 * 256
+
+    def ws(a, split=0):
+        return lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), split)
 
     B, Hq, Hk, M, N, D = 2, 8, 2, 300, 500, 64
     a = make_args(B, Hq, Hk, M, N, D)
     mpad = 384
-    want = 2 * r256(B * Hq * mpad * 4) + r256(B * Hq * N * 2 * D * 4)
-    assert lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0) == want
+    base = 2 * r256(B * Hq * mpad * 4) + r256(B * Hq * N * 2 * D * 4)
+    assert ws(a, 1) == base
+    assert ws(a) == base + r256(B * Hq * _ds_blocks(M, N, True) * 2048)
     a = make_args(64, 8, 4, 128, 128, 32)  # 64 * 4 * 1 = 256 workgroups: no partials
-    assert lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0) == \
-        2 * r256(64 * 8 * 128 * 4)
+    assert ws(a, 1) == 2 * r256(64 * 8 * 128 * 4)
     a = make_args(1, 4, 4, 100, 100, 128)  # MHA: no partials
-    assert lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0) == \
-        2 * r256(4 * 128 * 4)
+    assert ws(a, 1) == 2 * r256(4 * 128 * 4)
+    assert ws(a) == 2 * r256(4 * 128 * 4) + r256(4 * _ds_blocks(100, 100, True) * 2048)
+
+
+@pytest.mark.parametrize("M,N", [(300, 500), (500, 300), (1, 64), (130, 100), (2000, 40),
+                                 (40, 2000), (4096, 4096), (777, 1025), (100, 4000)])
+@pytest.mark.parametrize("causal", [1, 0])
+def test_attention_backward_ds_blocks(lib, M, N, causal):
+    """The library's closed-form count of stored dS blocks (per-row-block
+    prefix sums of clamped visible-block counts) against the count made block
+    by block, for M < N, M > N (rows with no key), ragged and tiny shapes."""
+    def r256(x):
+        return (x + 255) // 256 * 256
+
+    a = make_args(1, 2, 2, M, N, 64, causal=causal)
+    full = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0)
+    nods = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 1)
+    assert full - nods == r256(2 * _ds_blocks(M, N, causal) * 2048)
 
 
 def test_attention_entry_points_reject_bad_requests(lib):
@@ -139,8 +170,9 @@ def test_attention_entry_points_reject_bad_requests(lib):
     # forward: the normalizer output is required
     assert lib.fas_attention_forward(ctypes.byref(a), None, st3, None, 0, None) == _native.FAS_ERR_INVALID
     assert "fas_attention_forward" in _err(lib) and "lse" in _err(lib)
-    # backward: a NULL dout, a misaligned dk, a short workspace
-    need = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 0)
+    # backward: a NULL dout, a misaligned dk, a workspace short of the
+    # minimum (the size without the stored dS)
+    need = lib.fas_workspace_bytes(_native.VARIANT_ATTENTION_BACKWARD, ctypes.byref(a), 1)
     rc = lib.fas_attention_backward(ctypes.byref(a), None, st4, 0x10000, st3, 0x10000, st4,
                                     0x10000, kst, 0x10000, kst, 0x10000, need, None)
     assert rc == _native.FAS_ERR_INVALID and "dout is NULL" in _err(lib)
