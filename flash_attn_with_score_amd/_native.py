@@ -14,7 +14,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 DTYPE_CODES = {torch.float16: 0, torch.bfloat16: 1}
 

@@ -49,7 +49,7 @@
 extern "C" {
 #endif
 
-#define FAS_ABI_VERSION 7
+#define FAS_ABI_VERSION 8
 
 typedef enum fas_dtype {
   FAS_DTYPE_F16 = 0,
@@ -133,7 +133,10 @@ const char* fas_last_error(void);
 
 /* Device workspace (bytes, 256-byte aligned) an entry point of `variant`
  * needs for this problem; 0 when it needs none.  split is ignored by the
- * variants without one.  Returns (size_t)-1 for an invalid request. */
+ * variants without one, except FAS_VARIANT_ATTENTION_BACKWARD: there a
+ * nonzero split asks for the size without the stored dS (the smallest
+ * workspace the backward accepts).  Returns (size_t)-1 for an invalid
+ * request. */
 size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split);
 
 /* Replaces attention_with_scores.py:214-333 (+ _fwd_kernel_with_scores
@@ -252,12 +255,20 @@ int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t 
  * forward output O and lse its normalizer;
  * dout is dL/dO (shaped like out).  Writes dq (like q) and dk, dv
  * (B, Hk, N, D) in the input dtype, dk and dv summed over the Hq/Hk query
- * heads of each KV head.  Needs fas_workspace_bytes(
- * FAS_VARIANT_ATTENTION_BACKWARD, a, 0) bytes of workspace.  With dropout
- * and no keep_bits that size includes B*Hq*Mpad*ceil(N/32)*4 bytes (256-byte
- * aligned, Mpad = M rounded up to 128) of keep bits passed from the dK/dV
- * kernel to the dQ kernel; a workspace short of them (at least the rest)
- * makes both kernels evaluate the random stream, with the same result. */
+ * heads of each KV head.  The full workspace, fas_workspace_bytes(
+ * FAS_VARIANT_ATTENTION_BACKWARD, a, 0), includes dS in the input dtype for
+ * every 32 x 32 block of (query, key) pairs that holds a visible pair (2 KiB
+ * per block, rows padded to Mpad = M rounded up to 128; about B*Hq*M*N bytes
+ * causal): the dK/dV kernel stores it and the dQ kernel reads it instead of
+ * recomputing S and dP.  It is left out when it would pass 16 GiB or 2 GiB
+ * in one head, or when the workspace given is smaller than the full size but
+ * at least fas_workspace_bytes(FAS_VARIANT_ATTENTION_BACKWARD, a, 1); dk and
+ * dv are the same bits either way, dq agrees within rounding.  Without the
+ * stored dS, with dropout and no keep_bits, that smaller size includes
+ * B*Hq*Mpad*ceil(N/32)*4 bytes (256-byte aligned) of keep bits passed from
+ * the dK/dV kernel to the dQ kernel; a workspace short of them (at least the
+ * rest) makes both kernels evaluate the random stream, with the same
+ * result. */
 int fas_attention_backward(const fas_attn_args* a, const void* dout,
                            const int64_t dout_stride[4], const float* lse,
                            const int64_t lse_stride[3], void* dq, const int64_t dq_stride[4],

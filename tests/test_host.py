@@ -40,7 +40,7 @@ def header_functions():
 
 
 def test_library_loads_with_abi_version(lib):
-    assert lib.fas_abi_version() == _native.ABI_VERSION == 7
+    assert lib.fas_abi_version() == _native.ABI_VERSION == 8
     m = re.search(r"#define FAS_ABI_VERSION (\d+)", open(HEADER).read())
     assert m and int(m.group(1)) == _native.ABI_VERSION
 
