@@ -34,9 +34,11 @@ static hipError_t bwd_t(const BwdParams& p, hipStream_t s) {
   }
   if (p.M > 0) {
     const dim3 grid((unsigned)(bh * p.nrb));
-    if (p.ds)
-      hipLaunchKernelGGL((bwd_dq_ds_kernel<E, D>), grid, dim3(256), 0, s, p);
-    else if (!p.dropout)
+    if (p.ds) {
+      const int bm = 32 * kBwdDqDsWaves;
+      hipLaunchKernelGGL((bwd_dq_ds_kernel<E, D>), dim3((unsigned)(bh * ((p.Mpad + bm - 1) / bm))),
+                         dim3(64 * kBwdDqDsWaves), 0, s, p);
+    } else if (!p.dropout)
       hipLaunchKernelGGL((bwd_dq_kernel<E, D, 0>), grid, dim3(256), 0, s, p);
     else if (p.drop_bits)
       hipLaunchKernelGGL((bwd_dq_kernel<E, D, 2>), grid, dim3(256), 0, s, p);

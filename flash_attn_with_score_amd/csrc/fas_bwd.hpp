@@ -673,6 +673,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
 }
 
+constexpr int kBwdDqDsWaves = 8;  // waves (32 rows each) per bwd_dq_ds_kernel workgroup
+
 // dQ from the dS blocks the dK/dV kernel stored (p.ds): query-block outer, a
 // wave owns 32 rows and streams 64-key tiles; per tile the workgroup's K rows
 // and each wave's two dS blocks arrive in LDS by DMA, and
@@ -685,23 +687,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // mask hides were never stored and are not read.  No recomputation of S and
 // dP, no dropout (dS already carries it), and the same dS values as dK.
 //
-// The kernel is bound by the dS stream from HBM, so dS runs two tiles ahead
-// (three LDS stages) and K, mostly an L2 hit, one tile ahead (two stages):
-// 80 KiB of LDS, two workgroups per CU.  Every wave issues exactly four dS
-// DMAs per tile (blocks outside the visible range read from an offset past
-// the buffer: zeros, no memory traffic), after the tile's K DMAs, so
-// "vmcnt <= 4" at the end of a step means everything but the newest dS tile
-// has landed (vector loads complete in issue order).
+// The kernel is bound by the dS stream from HBM and by the latency of the K
+// tiles from L2, so both run two tiles ahead (three LDS stages each) for
+// 256-row workgroups of eight waves: 144 KiB of LDS, one workgroup per CU.
+// Every wave issues its K DMAs and then exactly four dS DMAs per tile
+// (blocks outside the visible range read from an offset past the buffer:
+// zeros, no memory traffic), so at the end of a step "vmcnt <= this wave's
+// DMA count of one tile" means everything but the newest tile has landed
+// (vector loads complete in issue order).
 template <class E, int D>
-__global__ __launch_bounds__(256) void bwd_dq_ds_kernel(const BwdParams p) {
+__global__ __launch_bounds__(512) void bwd_dq_ds_kernel(const BwdParams p) {
   constexpr int DB = D >= 32 ? D / 32 : 1;
-  constexpr int NW = 4;
+  constexpr int NW = kBwdDqDsWaves;
   constexpr int BM = 32 * NW;     // query rows per workgroup
   constexpr int BN = 64;          // keys per tile
   constexpr int TILE = BN * D;
   constexpr int STILE = BN * 32;  // a wave's dS^T tile
+  constexpr int KBLK = TILE / 512;  // 1 KiB K blocks per tile, dealt to the waves
 
-  __shared__ __attribute__((aligned(16))) uint16_t klds[2][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t klds[3][TILE];
   __shared__ __attribute__((aligned(16))) uint16_t slds[3][NW][STILE];
 
   const int tid = threadIdx.x;
@@ -710,12 +714,13 @@ __global__ __launch_bounds__(256) void bwd_dq_ds_kernel(const BwdParams p) {
   // Workgroup i runs on XCD i % 8: each XCD takes a contiguous run of
   // (head, row block) pairs, head-major, so the workgroups running at once
   // on one XCD share a head or two and their K rows stay in its L2.
-  const int total = p.B * p.H * p.nrb;
+  const int nrb = (p.Mpad + BM - 1) / BM;
+  const int total = (int)gridDim.x;
   int bid = blockIdx.x;
   if (total % 8 == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-  const int bh = bid / p.nrb;
-  int rb = bid % p.nrb;
-  if (p.causal) rb = p.nrb - 1 - rb;  // longest row blocks first
+  const int bh = bid / nrb;
+  int rb = bid % nrb;
+  if (p.causal) rb = nrb - 1 - rb;  // longest row blocks first
   const int b = bh / p.H, h = bh % p.H, hk = h / p.G;
   const int row0 = rb * BM, wrow0 = row0 + 32 * wave;
 
@@ -744,11 +749,10 @@ __global__ __launch_bounds__(256) void bwd_dq_ds_kernel(const BwdParams p) {
     const int ch = (lane & 3) ^ swz<32>(key);
     goff[i] = (uint32_t)((key >> 5) * 2048 + (ch >> 1) * 1024 + ((key & 31) + 32 * (ch & 1)) * 16);
   }
-  auto fetch_k = [&](int t) __attribute__((always_inline)) {
-    dma_tile<D, BN, NW>(wk, p.sk2, t * BN, k_base + (uint32_t)((t & 1) * TILE * 2), wave, lane);
-  };
-  auto fetch_s = [&](int t) __attribute__((always_inline)) {
-    const uint32_t lb = s_base + (uint32_t)((t % 3) * NW * STILE * 2);
+  auto fetch = [&](int t) __attribute__((always_inline)) {
+    const int st = t % 3;
+    dma_tile<D, BN, NW>(wk, p.sk2, t * BN, k_base + (uint32_t)(st * TILE * 2), wave, lane);
+    const uint32_t lb = s_base + (uint32_t)(st * NW * STILE * 2);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool vis = 2 * t + (i >> 1) < wblk;
@@ -756,12 +760,22 @@ __global__ __launch_bounds__(256) void bwd_dq_ds_kernel(const BwdParams p) {
                lb + 1024u * (uint32_t)i);
     }
   };
-  // Everything issued except the newest tile's four dS DMAs (if any).
+  // Wait for everything but the newest tile's DMAs (ahead) or for all.
   auto wait_ahead = [&](bool ahead) __attribute__((always_inline)) {
-    if (ahead)
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else
+    if (!ahead) {
       vm_wait_all();
+    } else if constexpr (KBLK >= NW) {
+      static_assert(KBLK % NW == 0 && KBLK / NW <= 2, "K DMA count per wave");
+      if constexpr (KBLK / NW == 2)
+        asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    } else {
+      if (wave < KBLK)
+        asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    }
   };
 
   f32x16 dq[DB];
@@ -771,16 +785,14 @@ __global__ __launch_bounds__(256) void bwd_dq_ds_kernel(const BwdParams p) {
   const VtOff vts = vt_offsets<32>(lane);
 
   if (ntiles > 0) {
-    fetch_k(0);
-    fetch_s(0);
-    if (ntiles > 1) fetch_s(1);
+    fetch(0);
+    if (ntiles > 1) fetch(1);
     wait_ahead(ntiles > 1);
     __syncthreads();
   }
   for (int t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) fetch_k(t + 1);
-    if (t + 2 < ntiles) fetch_s(t + 2);
-    const uint16_t* kt = klds[t & 1];
+    if (t + 2 < ntiles) fetch(t + 2);
+    const uint16_t* kt = klds[t % 3];
     const uint16_t* st = slds[t % 3][wave];
 #pragma unroll
     for (int kb2 = 0; kb2 < 2; ++kb2) {
