@@ -114,6 +114,28 @@ def test_attention_backward_both_dq_routes(case, monkeypatch, gpu):
     assert_out_close(dv0, ref["dv"], "dv")
 
 
+@pytest.mark.parametrize("shape", [(1, 8, 8, 2048, 2048, 128, True), (2, 8, 2, 1000, 3000, 64, False),
+                                   (1, 16, 4, 3000, 1000, 32, True)],
+                         ids=lambda s: "B{}H{}K{}M{}N{}D{}{}".format(*s[:6], "c" if s[6] else "f"))
+def test_attention_backward_bit_reproducible(shape, gpu):
+    """Three backward passes of one forward give dq, dk and dv equal bit for
+    bit: no atomics, and every LDS stage of the pipelined kernels (the dQ
+    kernel keeps two tiles of K and dS in flight) is complete before it is
+    read.  Shapes with many key tiles per workgroup, GQA and M != N."""
+    B, Hq, Hk, M, N, D, causal = shape
+    print(f"[case] backward reproducible {shape}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=torch.float16, seed=11, device=gpu)
+    do = torch.randn(q.shape, generator=torch.Generator("cpu").manual_seed(12)).half().to(gpu)
+    qd, kd, vd = (t.requires_grad_(True) for t in (q, k, v))
+    o = fas.attention(qd, kd, vd, causal=causal)
+    runs = [torch.autograd.grad(o, (qd, kd, vd), do, retain_graph=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    for name, i in (("dq", 0), ("dk", 1), ("dv", 2)):
+        assert not torch.isnan(runs[0][i]).any(), name
+        for r in runs[1:]:
+            assert torch.equal(runs[0][i], r[i]), name
+
+
 def test_attention_large_magnitude_inputs(gpu):
     """q, k, v ~ N(0, 6^2): nearly one-hot softmax rows whose two half-waves
     see very different maxima."""
