@@ -711,15 +711,22 @@ __global__ __launch_bounds__(512) void bwd_dq_ds_kernel(const BwdParams p) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
-  // Workgroup i runs on XCD i % 8: each XCD takes a contiguous run of
-  // (head, row block) pairs, head-major, so the workgroups running at once
-  // on one XCD share a head or two and their K rows stay in its L2.
+  // Workgroup i runs on XCD i % 8: each XCD takes the row blocks of its own
+  // B*H/8 heads (their K rows stay in its L2), row-block major and, under a
+  // causal mask, longest first across those heads, so the CUs that finish
+  // short blocks take the next-longest ones (heads one after another instead
+  // left CUs that had finished mid-length blocks with full-length ones: 160
+  // against 120 us at B1 H32 S4096 D128 causal).
   const int nrb = (p.Mpad + BM - 1) / BM;
   const int total = (int)gridDim.x;
+  const int nbh = total / nrb;
   int bid = blockIdx.x;
-  if (total % 8 == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-  const int bh = bid / nrb;
-  int rb = bid % nrb;
+  const bool xcd = total % 8 == 0 && nbh % 8 == 0;
+  if (xcd) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+  const int per = xcd ? nbh / 8 : nbh;  // heads per XCD
+  const int run = bid / (per * nrb), idx = bid % (per * nrb);
+  const int bh = run * per + idx % per;
+  int rb = idx / per;
   if (p.causal) rb = nrb - 1 - rb;  // longest row blocks first
   const int b = bh / p.H, h = bh % p.H, hk = h / p.G;
   const int row0 = rb * BM, wrow0 = row0 + 32 * wave;
