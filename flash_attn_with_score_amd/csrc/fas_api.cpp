@@ -389,26 +389,43 @@ int64_t bwd_ds_head(const Problem& pr) {
 // Largest dS workspace the backward takes (all heads); past it, and when one
 // head's blocks reach 2 GiB, the dQ kernel recomputes S and dP instead.
 constexpr size_t kBwdDsMaxBytes = (size_t)16 << 30;
+size_t bwd_ds_bytes(const Problem& pr) {
+  return align256((size_t)pr.B * pr.H * (size_t)bwd_ds_head(pr) * 2048);
+}
+// Whether the backward stores dS when the caller's workspace has room.
+bool bwd_ds_fits(const Problem& pr) {
+  return pr.M > 0 && pr.N > 0 && bwd_ds_head(pr) * 2048 < ((int64_t)1 << 31) &&
+         bwd_ds_bytes(pr) <= kBwdDsMaxBytes;
+}
 
 // The caller's keep-bit buffer (fas_attn_args.keep_bits) of attention's
 // forward and backward: key-major words for the dK/dV kernel (word
-// ((b*H + h) * ceil(M/32) + i/32) * N + j, bit i % 32), then 32-row blocks
-// of row-major words for the dQ kernel (the backward's own layout, rows
-// padded to Mpad).  Each head's part must stay below 2 GiB (32-bit buffer
-// offsets); otherwise no buffer is used.
+// ((b*H + h) * ceil(M/32) + i/32) * N + j, bit i % 32), then, only when the
+// backward cannot store dS, 32-row blocks of row-major words for the dQ
+// kernel that recomputes S and dP (the backward's own layout, rows padded
+// to Mpad).  Each head's part must stay below 2 GiB (32-bit buffer
+// offsets); otherwise no buffer (key-major part) or no row blocks.
 struct KeepLayout {
   size_t keys = 0, rows = 0, total = 0;  // byte offsets / total
   bool ok = false;
+  bool has_rows = false;
 };
 KeepLayout keep_layout(const Problem& pr) {
   KeepLayout k;
   const size_t head_keys = (size_t)((pr.M + 31) / 32) * pr.N * 4;
   const size_t head_rows = (size_t)bwd_mpad(pr) * ((pr.N + 31) / 32) * 4;
-  if (!pr.dropout || head_keys >= ((size_t)1 << 31) || head_rows >= ((size_t)1 << 31)) return k;
+  if (!pr.dropout || head_keys >= ((size_t)1 << 31)) return k;
   k.keys = 0;
-  k.rows = align256((size_t)pr.B * pr.H * head_keys);
-  k.total = k.rows + align256((size_t)pr.B * pr.H * head_rows);
+  k.total = align256((size_t)pr.B * pr.H * head_keys);
   k.ok = true;
+  // The row blocks serve only the dQ kernel that recomputes S and dP: none
+  // when the backward can store dS (a backward that then takes the recompute
+  // route anyway evaluates the random stream for dQ, with the same result).
+  if (!bwd_ds_fits(pr) && head_rows < ((size_t)1 << 31)) {
+    k.rows = k.total;
+    k.total += align256((size_t)pr.B * pr.H * head_rows);
+    k.has_rows = true;
+  }
   return k;
 }
 
@@ -487,13 +504,11 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
     // when a head's blocks stay below 2 GiB, all of them within
     // kBwdDsMaxBytes and the caller's workspace has room for them
     // (fas_workspace_bytes includes them unless asked with split != 0).
-    const int64_t ds_head = bwd_ds_head(pr);
-    const size_t ds_bytes = align256((size_t)pr.B * pr.H * (size_t)ds_head * 2048);
-    if (split == 0 && pr.M > 0 && pr.N > 0 && ds_head * 2048 < ((int64_t)1 << 31) &&
-        ds_bytes <= kBwdDsMaxBytes && off + ds_bytes <= budget) {
+    const size_t ds_bytes = bwd_ds_bytes(pr);
+    if (split == 0 && bwd_ds_fits(pr) && off + ds_bytes <= budget) {
       w.has_ds = true;
       w.ds = off;
-      w.ds_head = ds_head;
+      w.ds_head = bwd_ds_head(pr);
       off += ds_bytes;
     }
     // Without stored dS, with dropout, the dK/dV kernel stores its keep
@@ -979,7 +994,7 @@ int fas_attention_forward(const fas_attn_args* a, float* lse, const int64_t st[3
   p.sl2 = st[2];
   if (pr.keep) {
     p.drop_bits = at<uint32_t>(a->keep_bits, kl.keys);
-    p.drop_rows = at<uint32_t>(a->keep_bits, kl.rows);
+    if (kl.has_rows) p.drop_rows = at<uint32_t>(a->keep_bits, kl.rows);
     p.rows32 = (int)(bwd_mpad(pr) / 32);
   }
   return run_fwd(fn, p, pr, pr.keep ? fas::kFwdPlainKeepBits : fas::kFwdPlain, stream);
@@ -1095,7 +1110,7 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   if (pr.keep) {
     // The forward's bits: dK/dV reads the key-major words, dQ the row blocks.
     p.keep_keys = at<uint32_t>(a->keep_bits, kl.keys);
-    p.drop_bits = at<uint32_t>(a->keep_bits, kl.rows);
+    p.drop_bits = kl.has_rows ? at<uint32_t>(a->keep_bits, kl.rows) : nullptr;
   }
   p.sm_scale = std::fabs(pr.sm_scale);
   p.scale_signed = pr.sm_scale;

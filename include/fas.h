@@ -118,7 +118,8 @@ typedef struct fas_attn_args {
   /* Optional, with dropout: a device buffer of
    * fas_workspace_bytes(FAS_VARIANT_KEEP_BITS, ...) bytes, 256-byte aligned,
    * owned by the caller.  fas_attention_forward stores the mask in it (one
-   * bit per pair, in the two layouts the backward kernels read);
+   * bit per pair, key-major for the dK/dV kernel, plus row blocks for the
+   * dQ kernel that recomputes S and dP when the backward cannot store dS);
    * fas_attention_backward given the same buffer and dropout fields reads
    * it instead of evaluating the random stream again.  NULL: both evaluate
    * the stream.  The other entry points ignore it.  This build's own

@@ -287,6 +287,40 @@ def test_attention_keep_bits_cap(monkeypatch, gpu):
         assert torch.equal(x, y), name
 
 
+def test_attention_dropout_both_dq_routes(monkeypatch, gpu):
+    """attention() with dropout, the forward keeping its (key-major) mask
+    bits: the default backward reads the stored dS in its dQ kernel; with
+    the workspace limited below the dS (FAS_BWD_WORKSPACE_MAX_BYTES) the dQ
+    kernel recomputes S and dP and, the forward having stored no row blocks
+    for it, evaluates the random stream.  O, dk and dv are the same bits on
+    both routes, dq of each is within the oracle tolerance (64-bit offset
+    carrying into counter word 1)."""
+    from flash_attn_with_score_amd import flash
+
+    B, H, Hk, M, N, D = 1, 4, 2, 200, 264, 64
+    seed, offset = 5151, 2**32 - 20_000
+    print(f"[case] attention dropout dq routes B{B}H{H}K{Hk}M{M}N{N}D{D}", flush=True)
+    q, k, v = inputs.make_qkv(B, H, Hk, M, N, D, dtype=torch.float16, seed=17)
+    do = torch.randn(q.shape, generator=torch.Generator("cpu").manual_seed(6)).half()
+    outs = []
+    for limit in (flash.BWD_WORKSPACE_MAX_BYTES, 0):
+        monkeypatch.setattr(flash, "BWD_WORKSPACE_MAX_BYTES", limit)
+        _set_state(gpu, seed, offset)
+        qg, kg, vg = (t.to(gpu).requires_grad_(True) for t in (q, k, v))
+        o = fas.attention(qg, kg, vg, causal=True, dropout_p=P)
+        outs.append((o, *torch.autograd.grad(o, (qg, kg, vg), do.to(gpu))))
+    torch.cuda.synchronize()
+    for name, x, y in zip(("o", "dq", "dk", "dv"), *outs):
+        assert not torch.isnan(x).any() and not torch.isnan(y).any(), name
+        if name != "dq":
+            assert torch.equal(x, y), name
+    r = naive.attention_reference(q, k, v, do, causal=True, dropout=(P, seed, offset))
+    assert_out_close(outs[0][1], r["dq"], "dq (stored dS)")
+    assert_out_close(outs[1][1], r["dq"], "dq (recomputed)")
+    assert_out_close(outs[0][2], r["dk"], "dk")
+    assert_out_close(outs[0][3], r["dv"], "dv")
+
+
 def test_attention_backward_without_bit_workspace(gpu):
     """fas_attention_backward with dropout and no keep_bits, on the route
     that recomputes S and dP for dQ (a workspace without the stored dS):

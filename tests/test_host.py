@@ -47,15 +47,22 @@ def test_library_loads_with_abi_version(lib):
 
 def test_keep_bits_size(lib):
     """FAS_VARIANT_KEEP_BITS sizes the caller's keep-bit buffer: with dropout,
-    B*Hq*(ceil(M/32)*N + Mpad*ceil(N/32))*4 bytes in two 256-byte-aligned
-    parts; 0 without dropout."""
+    B*Hq*ceil(M/32)*N*4 bytes of key-major words, plus B*Hq*Mpad*ceil(N/32)*4
+    of row blocks (256-byte-aligned parts) only when the backward cannot
+    store dS (more than 16 GiB of it); 0 without dropout."""
     q = torch.empty(2, 3, 100, 64, dtype=torch.float16)
     k = torch.empty(2, 3, 70, 64, dtype=torch.float16)
     a = _native.make_args(q, k, k, q, True, 0.125, (0.1, 1, 0))
     keys = 2 * 3 * 4 * 70 * 4                   # ceil(100/32) = 4 row words per key
-    rows = 2 * 3 * 128 * 3 * 4                  # Mpad 128, ceil(70/32) = 3 key words
     al = lambda x: (x + 255) // 256 * 256
-    assert lib.fas_workspace_bytes(_native.VARIANT_KEEP_BITS, ctypes.byref(a), 0) == al(keys) + al(rows)
+    assert lib.fas_workspace_bytes(_native.VARIANT_KEEP_BITS, ctypes.byref(a), 0) == al(keys)
+    # B1 H64 S32768 causal: 64 * 524,800 dS blocks of 2 KiB (68.8 GB) exceed
+    # 16 GiB, so the row blocks are included (sizes only, nothing allocated).
+    big = make_args(1, 64, 64, 32768, 32768, 64)
+    big.dropout_p, big.dropout_seed = 0.1, 1
+    keys = 64 * 1024 * 32768 * 4
+    rows = 64 * 32768 * 1024 * 4
+    assert lib.fas_workspace_bytes(_native.VARIANT_KEEP_BITS, ctypes.byref(big), 0) == al(keys) + al(rows)
     b = _native.make_args(q, k, k, q, True, 0.125)
     assert lib.fas_workspace_bytes(_native.VARIANT_KEEP_BITS, ctypes.byref(b), 0) == 0
 
