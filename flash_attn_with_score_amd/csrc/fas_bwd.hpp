@@ -680,8 +680,10 @@ constexpr int kBwdDqDsWaves = 8;  // waves (32 rows each) per bwd_dq_ds_kernel w
 // and each wave's two dS blocks arrive in LDS by DMA, and
 //   dQ^T += K^T dS^T
 // takes both operands from LDS with the transposing read.  The dS blocks
-// are stored key-major (lane = key, eight rows per 16 bytes), so the DMA
-// gathers them into a swizzled [64 keys][32 rows] tile, whose transposing
+// are stored as the dK/dV kernel's B-operand fragments (lane l of a 2 KiB
+// block: key l % 32, eight consecutive rows per 16 bytes, at 16 l and
+// 1024 + 16 l), so the DMA gathers them into a swizzled [64 keys][32 rows]
+// tile, whose transposing
 // read yields rows on lanes and eight consecutive keys per lane, the B
 // operand; lane c then holds row perm_row(c) of the wave.  Blocks a causal
 // mask hides were never stored and are not read.  No recomputation of S and
@@ -704,6 +706,7 @@ __global__ __launch_bounds__(512) void bwd_dq_ds_kernel(const BwdParams p) {
   constexpr int TILE = BN * D;
   constexpr int STILE = BN * 32;  // a wave's dS^T tile
   constexpr int KBLK = TILE / 512;  // 1 KiB K blocks per tile, dealt to the waves
+  static_assert(KBLK % NW == 0 || NW % KBLK == 0, "K DMA blocks per wave");
 
   __shared__ __attribute__((aligned(16))) uint16_t klds[3][TILE];
   __shared__ __attribute__((aligned(16))) uint16_t slds[3][NW][STILE];
