@@ -85,7 +85,19 @@ def test_attention_forward_and_backward(case, dtype, gpu):
     assert_out_close(dv, ref["dv"], "dv")
 
 
-@pytest.mark.parametrize("case", CASES, ids=_label)
+# Edge shapes for the dS block layout: one key, lengths just off 32 and 256,
+# M > N with rows that see no key, and a batch of several heads.
+EDGE_CASES = [
+    (1, 2, 2, 64, 1, 64, False, None),
+    (1, 2, 2, 64, 1, 64, True, None),
+    (1, 4, 1, 33, 31, 16, True, None),
+    (3, 2, 2, 257, 255, 128, True, None),
+    (2, 6, 3, 31, 289, 32, True, None),
+    (1, 2, 2, 300, 40, 64, True, None),
+]
+
+
+@pytest.mark.parametrize("case", CASES + EDGE_CASES, ids=_label)
 def test_attention_backward_both_dq_routes(case, monkeypatch, gpu):
     """The backward's two dQ routes: from the dS blocks the dK/dV kernel
     stores (the default workspace) and, with the workspace limited below
