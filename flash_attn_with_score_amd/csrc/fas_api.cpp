@@ -43,21 +43,32 @@ int hip_status(const char* fn, hipError_t e) {
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
 constexpr int64_t kMaxSliceBytes = (int64_t)1 << 31;
+// Largest batch or head stride (elements): 2^46 two-byte elements span 128
+// TiB, beyond any device's address space, and keep every offset product of
+// the kernels (index * stride, index < 2^24) inside int64.
+constexpr int64_t kMaxOuterStride = (int64_t)1 << 46;
 
 // Checks one (B, H, L, D)-shaped 16-bit tensor: innermost stride 1, 16-byte
 // aligned rows, and a (batch, head) slice addressable with 32-bit offsets
-// (including the tile overhang the kernels read past the last row).
+// (including the tile overhang the kernels read past the last row).  Each
+// bound is tested before the product that uses it, so no arithmetic here
+// can overflow whatever strides the caller passes.
 int check_tensor(const char* fn, const char* name, const void* ptr, const int64_t* st, int64_t rows,
                  int64_t D) {
   if (ptr == nullptr) return fail(FAS_ERR_INVALID, fn, "%s is NULL", name);
   if (st[3] != 1)
     return fail(FAS_ERR_INVALID, fn, "%s innermost stride must be 1 (got %lld)", name,
                 (long long)st[3]);
+  if (st[0] < 0 || st[1] < 0 || st[2] < 0)
+    return fail(FAS_ERR_INVALID, fn, "%s has a negative stride", name);
   if (!aligned16(ptr) || st[0] % 8 || st[1] % 8 || st[2] % 8)
     return fail(FAS_ERR_INVALID, fn,
                 "%s rows must be 16-byte aligned (pointer and outer strides multiples of 8)", name);
   if (st[2] < D) return fail(FAS_ERR_INVALID, fn, "%s rows overlap (row stride < head_dim)", name);
-  if ((rows + 512) * st[2] * 2 >= kMaxSliceBytes)
+  if (st[0] >= kMaxOuterStride || st[1] >= kMaxOuterStride)
+    return fail(FAS_ERR_UNSUPPORTED, fn, "%s batch or head stride exceeds 2^46 elements", name);
+  // rows <= 2^28 (check_shape), so with st[2] < 2^31 the product fits.
+  if (st[2] >= kMaxSliceBytes || (rows + 512) * st[2] * 2 >= kMaxSliceBytes)
     return fail(FAS_ERR_UNSUPPORTED, fn, "%s (batch, head) slice exceeds 2 GiB", name);
   return FAS_OK;
 }
@@ -127,8 +138,18 @@ int check_shape(const char* fn, const fas_attn_args* a, Problem* pr) {
   if (a->heads_q % a->heads_k != 0)
     return fail(FAS_ERR_INVALID, fn, "heads_q (%lld) is not a multiple of heads_k (%lld)",
                 (long long)a->heads_q, (long long)a->heads_k);
-  if (a->seqlen_q > (1 << 28) || a->seqlen_k > (1 << 28) || a->batch * a->heads_q > (1 << 24))
+  // Bounds that keep every index of the kernels inside 32 bits and every
+  // size and offset product of the host code inside 64 (heads_q is tested
+  // alone first so that batch * heads_q cannot overflow).
+  if (a->seqlen_q > (1 << 28) || a->seqlen_k > (1 << 28) || a->heads_q > (1 << 24) ||
+      a->batch > (1 << 24) || a->batch * a->heads_q > (1 << 24))
     return fail(FAS_ERR_UNSUPPORTED, fn, "sizes exceed the index range of the kernels");
+  // The largest workspace term is 4 bytes per (query, key) pair (the
+  // buffered cross softmax sum's region): past 2^58 pairs its size would
+  // not fit a size_t.
+  if ((unsigned __int128)a->batch * a->heads_q * a->seqlen_q * a->seqlen_k >
+      ((unsigned __int128)1 << 58))
+    return fail(FAS_ERR_UNSUPPORTED, fn, "B*Hq*M*N exceeds 2^58 (query, key) pairs");
   if (!std::isfinite(a->sm_scale)) return fail(FAS_ERR_INVALID, fn, "sm_scale is not finite");
   if (!(a->dropout_p >= 0.f && a->dropout_p < 1.f))
     return fail(FAS_ERR_INVALID, fn, "dropout_p %g outside [0, 1)", (double)a->dropout_p);
@@ -277,9 +298,18 @@ int run_fwd(const char* fn, fas::FwdParams& p, const Problem& pr, int mode, void
   return hip_status(fn, fas::launch_fwd(p, mode, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
 }
 
+// Whether one of the first n strides is negative or past kMaxOuterStride.
+bool strides_out_of_range(const int64_t* st, int n) {
+  for (int i = 0; i < n; ++i)
+    if (st[i] < 0 || st[i] >= kMaxOuterStride) return true;
+  return false;
+}
+
 int check_out3(const char* fn, const char* name, const float* out, const int64_t* st) {
   if (out == nullptr) return fail(FAS_ERR_INVALID, fn, "%s is NULL", name);
   if (st == nullptr) return fail(FAS_ERR_INVALID, fn, "%s strides are NULL", name);
+  if (strides_out_of_range(st, 3))
+    return fail(FAS_ERR_INVALID, fn, "%s strides must lie in [0, 2^46)", name);
   return FAS_OK;
 }
 
@@ -755,14 +785,21 @@ int fas_abi_version(void) { return FAS_ABI_VERSION; }
 const char* fas_last_error(void) { return g_last_error.c_str(); }
 
 size_t fas_workspace_bytes(int variant, const fas_attn_args* a, int64_t split) {
+  static const char* fn = "fas_workspace_bytes";
   Problem pr;
-  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_KEEP_BITS) return (size_t)-1;
-  if (check_shape("fas_workspace_bytes", a, &pr)) return (size_t)-1;
+  if (variant < FAS_VARIANT_SCORES || variant > FAS_VARIANT_KEEP_BITS) {
+    fail(FAS_ERR_INVALID, fn, "variant %d unknown", variant);
+    return (size_t)-1;
+  }
+  if (check_shape(fn, a, &pr)) return (size_t)-1;
   if (variant == FAS_VARIANT_KEEP_BITS) return keep_layout(pr).total;
   const bool has_split = variant == FAS_VARIANT_CROSS_QK_SUM ||
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM ||
                          variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED;
-  if (has_split && !(split > 0 && split <= pr.N)) return (size_t)-1;
+  if (has_split && !(split > 0 && split <= pr.N)) {
+    fail(FAS_ERR_INVALID, fn, "split %lld outside (0, %d]", (long long)split, pr.N);
+    return (size_t)-1;
+  }
   // The backward: split != 0 asks for the size without the stored dS.
   const bool bwd = variant == FAS_VARIANT_ATTENTION_BACKWARD;
   // The key-split plan depends on the GQA packing, which a launch picks
@@ -782,6 +819,8 @@ static int check_scores_out(const char* fn, const void* scores, const int64_t* s
   if (st[3] != 1) return fail(FAS_ERR_INVALID, fn, "scores innermost stride must be 1");
   if (reinterpret_cast<uintptr_t>(scores) & 1u)
     return fail(FAS_ERR_INVALID, fn, "scores is not 2-byte aligned");
+  if (strides_out_of_range(st, 3))
+    return fail(FAS_ERR_INVALID, fn, "scores strides must lie in [0, 2^46)");
   if ((int64_t)fas::kFwdRows * st[2] * 2 >= kMaxSliceBytes)
     return fail(FAS_ERR_UNSUPPORTED, fn, "score rows too long for 32-bit offsets");
   return FAS_OK;
@@ -937,7 +976,9 @@ int fas_attention_with_softmax_col_sum_noalloc(const fas_attn_args* a, float* co
   static const char* fn = "fas_attention_with_softmax_col_sum_noalloc";
   Problem pr;
   int rc;
-  if ((rc = check_shape(fn, a, &pr))) return rc;
+  // Every argument check first: the scratch lookup below is a HIP call.
+  if ((rc = check_args(fn, a, &pr))) return rc;
+  if ((rc = check_out3(fn, "sum output", col_sum, st))) return rc;
   // The layout is bounded by the scratch: a key split that would not fit
   // takes fewer, longer splits (or none); what remains must fit.
   const Workspace w = layout(FAS_VARIANT_SOFTMAX_COL_SUM, pr, 0, kNoAllocScratchBytes);
@@ -1010,6 +1051,8 @@ int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t 
   if ((rc = check_out3(fn, "total", total, tst))) return rc;
   if (pr.M == 0) return zero_out3(fn, total, tst, pr.B, pr.H, pr.N, stream);
   if (lse == nullptr || lst == nullptr) return fail(FAS_ERR_INVALID, fn, "lse is NULL");
+  if (strides_out_of_range(lst, 3))
+    return fail(FAS_ERR_INVALID, fn, "lse strides must lie in [0, 2^46)");
   if ((rc = check_tensor(fn, "q", a->q, a->q_stride, pr.M, pr.D))) return rc;
   if ((rc = check_tensor(fn, "k", a->k, a->k_stride, pr.N, pr.D))) return rc;
   fas::ColsmParams c{};
@@ -1047,6 +1090,8 @@ int fas_attention_backward(const fas_attn_args* a, const void* dout, const int64
   if (pr.M > 0) {
     if (gst == nullptr || qst == nullptr || lst == nullptr || lse == nullptr)
       return fail(FAS_ERR_INVALID, fn, "dout, dq or lse is NULL");
+    if (strides_out_of_range(lst, 3))
+      return fail(FAS_ERR_INVALID, fn, "lse strides must lie in [0, 2^46)");
     if ((rc = check_tensor(fn, "dout", dout, gst, pr.M, pr.D))) return rc;
     if ((rc = check_tensor(fn, "dq", dq, qst, pr.M, pr.D))) return rc;
   }

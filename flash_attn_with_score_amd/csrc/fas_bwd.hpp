@@ -266,8 +266,14 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) pr[r] = exp2f_fast(fmaf(s[r], qk, nl[r]));
         if (!full) {
-          // Row r0 + acc_row(r, g) sees key key0 + c iff acc_row(r, g) >= lim.
-          const int lim = key0 + c - p.causal_off - r0;
+          // Row r0 + acc_row(r, g) sees key key0 + c iff acc_row(r, g) >= lim;
+          // keys past N see no row (lim 32).  Without that their weight
+          // would be exp2(nl[row]) (s = 0 from the zero K rows), whose dS
+          // can round to inf in the input type and turn the dQ product over
+          // the stored blocks into inf * 0.
+          const int lim = key0 + c >= p.N ? 32
+                          : p.causal     ? key0 + c - p.causal_off - r0
+                                         : -32;
 #pragma unroll
           for (int r = 0; r < 16; ++r)
             if (acc_row(r, g) < lim) pr[r] = 0.f;
@@ -353,9 +359,9 @@ __global__ __launch_bounds__(256) void bwd_dkdv_kernel(const BwdParams p) {
       for (int qb = 0; qb < 2; ++qb) {
         const int r0 = t * TQ + 32 * qb;
         // Live if the block's last row sees the wave's first key, full if its
-        // first row sees the wave's last key.
+        // first row sees the wave's last key and every key lies below N.
         const bool live = !p.causal || p.causal_off + r0 + 31 >= key0;
-        const bool full = !p.causal || p.causal_off + r0 >= key0 + 31;
+        const bool full = (!p.causal || p.causal_off + r0 >= key0 + 31) && key0 + 31 < p.N;
         if (live) body(qb, full);
       }
       if (more) {

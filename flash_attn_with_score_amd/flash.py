@@ -24,18 +24,24 @@ from . import _common, _native
 __all__ = ["attention", "FlashAttention"]
 
 # Largest keep-bit buffer (bytes) a forward with dropout holds for its
-# backward pass, about B*Hq*M*N/4; past it the backward evaluates the random
-# stream again, as the reference does.  FAS_KEEP_BITS_MAX_BYTES overrides it
-# (0 turns the buffer off).
-KEEP_BITS_MAX_BYTES = int(os.environ.get("FAS_KEEP_BITS_MAX_BYTES", 512 << 20))
+# backward pass, about B*Hq*M*N/8 (one bit per pair); past it the backward
+# evaluates the random stream again, as the reference does.  The buffer lives
+# from a layer's forward to its backward, so a model holds one per layer:
+# the default, 64 MiB, covers B1 H32 S4096 and keeps deeper or longer models
+# near the reference's O(M) saved state per head.  FAS_KEEP_BITS_MAX_BYTES
+# overrides it (0 turns the buffer off).
+KEEP_BITS_MAX_BYTES = int(os.environ.get("FAS_KEEP_BITS_MAX_BYTES", 64 << 20))
 
 # Largest workspace (bytes) the backward pass allocates.  The full size holds
 # dS in the input dtype for every visible (query, key) pair, about B*Hq*M*N
-# bytes causal and twice that without a mask (at most 16 GiB, a limit of the
-# library), which the dQ kernel reads instead of recomputing S and dP; past
-# this limit the backward takes the smaller workspace and recomputes.
-# FAS_BWD_WORKSPACE_MAX_BYTES overrides it (0: always recompute).
-BWD_WORKSPACE_MAX_BYTES = int(os.environ.get("FAS_BWD_WORKSPACE_MAX_BYTES", 16 << 30))
+# bytes causal and twice that without a mask, which the dQ kernel reads
+# instead of recomputing S and dP; past this limit (or when the allocation
+# fails) the backward takes the smaller workspace, O(B*Hq*M) bytes, and
+# recomputes.  The default, 1 GiB, holds the dS of B1 H32 S4096 causal
+# (541 MB, a 7% faster backward there); B1 H32 S16384 (8.6 GB of dS) then
+# recomputes at 3% more time.  FAS_BWD_WORKSPACE_MAX_BYTES overrides it
+# (0: always recompute; the library's own limit is 16 GiB).
+BWD_WORKSPACE_MAX_BYTES = int(os.environ.get("FAS_BWD_WORKSPACE_MAX_BYTES", 1 << 30))
 
 
 def _check_inputs(q, k, v):
@@ -118,8 +124,13 @@ class FlashAttention(torch.autograd.Function):
         # read from the forward's bits when it kept them.
         args = _native.make_args(q, k, v, o, ctx.causal, ctx.sm_scale, ctx.drop,
                                  ctx.keep_ptr if ctx.keep_buf is not None else 0)
-        ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args, 0,
-                                                 q.device, limit=BWD_WORKSPACE_MAX_BYTES)
+        try:
+            ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args, 0,
+                                                     q.device, limit=BWD_WORKSPACE_MAX_BYTES)
+        except torch.cuda.OutOfMemoryError:
+            # The stored dS is an optimisation: without room for it the
+            # backward recomputes S and dP in the dQ kernel.
+            ws_ptr, ws_bytes, ws = 0, 1, None
         if ws is None and ws_bytes > 0:
             # Over the limit: the workspace without the stored dS (split != 0).
             ws_ptr, ws_bytes, ws = _common.workspace(_native.VARIANT_ATTENTION_BACKWARD, args,

@@ -228,7 +228,13 @@ def oracle_for(entry_point: str, q, k, v, *, causal: bool, sm_scale=None, split=
                chunk: int = 1024, dropout=None) -> tuple[torch.Tensor, torch.Tensor]:
     """(out, side product) the named entry point must reproduce; dropout is
     None or (p, seed, offset) as the launch drew it.  The buffered cross
-    softmax sum ignores dropout (attention_cross_token_softmax_sum.py:639-732)."""
+    softmax sum ignores dropout (attention_cross_token_softmax_sum.py:639-732).
+    For rows with no admissible key (M > N, causal) the buffered entry point is
+    held to the fused kernel's convention, output 0
+    (attention_cross_token_softmax_sum.py:182-184): the reference's buffered
+    kernel writes acc * (1 / l_i) with l_i = 0 there (:498-503, :630), NaN,
+    a deviation this build makes on purpose.  Its sums mask those rows in
+    both kernels (:609-620), so the side product is the same either way."""
     side = ENTRY_POINT_OUTPUT[entry_point]
     if entry_point == "attention_cross_token_softmax_sum_buffered":
         dropout = None

@@ -126,6 +126,56 @@ def test_attention_backward_both_dq_routes(case, monkeypatch, gpu):
     assert_out_close(dv0, ref["dv"], "dv")
 
 
+def _aligned_qkv(M, N, D, dtype, v_zero, seed):
+    """q and k share a large common direction (q.k ~ 144 +- 17 at D = 64),
+    so with a negative sm_scale every score of a row is strongly negative and
+    so is its normalizer L."""
+    g = torch.Generator("cpu").manual_seed(seed)
+    a = 1.5 * torch.ones(D)
+    q = (a + torch.randn(1, 2, M, D, generator=g)).to(dtype)
+    k = (a + torch.randn(1, 2, N, D, generator=g)).to(dtype)
+    v = (torch.zeros(1, 2, N, D) if v_zero else torch.randn(1, 2, N, D, generator=g)).to(dtype)
+    return q, k, v
+
+
+# (dtype, sm_scale, v_zero): at -0.14 the rows' L lies in [-28, -10], so
+# exp(-L) * delta passes the fp16 range; at -1.0 L < -88 and exp(-L) passes
+# the fp32 range (V = 0 keeps every valid dS exactly 0, so dq must be 0).
+KEY_EDGE = [
+    (torch.float16, -0.14, False),
+    (torch.float16, -1.0, True),
+    (torch.bfloat16, -1.0, True),
+]
+
+
+@pytest.mark.parametrize("N", [1, 40])
+@pytest.mark.parametrize("dt,sm_scale,v_zero", KEY_EDGE,
+                         ids=["f16-scale0.14", "f16-scale1-v0", "bf16-scale1-v0"])
+def test_attention_dq_keys_past_n_strongly_negative_lse(N, dt, sm_scale, v_zero, monkeypatch, gpu):
+    """Non-causal, N % 32 != 0, rows whose normalizer L is strongly negative.
+    A key past N has a zero K row, so its unmasked weight would be
+    exp(-L): its dS then overflows the input type (or fp32) and the dQ
+    product over the stored dS blocks gives inf * 0 = NaN.  The dK/dV kernel
+    masks keys past N, so both dQ routes stay finite and match the oracle."""
+    from flash_attn_with_score_amd import flash
+
+    M, D = 64, 64
+    print(f"[case] dq keys past N: N{N} {dt} scale {sm_scale} v_zero {v_zero}", flush=True)
+    q, k, v = _aligned_qkv(M, N, D, dt, v_zero, seed=21)
+    do = torch.randn(1, 2, M, D, generator=torch.Generator("cpu").manual_seed(22)).to(dt)
+    ref = naive.attention_reference(q, k, v, do, causal=False, sm_scale=sm_scale)
+    for limit in (flash.BWD_WORKSPACE_MAX_BYTES, 0):
+        monkeypatch.setattr(flash, "BWD_WORKSPACE_MAX_BYTES", limit)
+        qd, kd, vd = (t.to(gpu).requires_grad_(True) for t in (q, k, v))
+        o = fas.attention(qd, kd, vd, causal=False, sm_scale=sm_scale)
+        dq, dk, dv = torch.autograd.grad(o, (qd, kd, vd), do.to(gpu))
+        torch.cuda.synchronize()
+        route = "stored dS" if limit else "recomputed"
+        assert_out_close(dq, ref["dq"], f"dq ({route})")
+        assert_out_close(dk, ref["dk"], f"dk ({route})")
+        assert_out_close(dv, ref["dv"], f"dv ({route})")
+
+
 @pytest.mark.parametrize("shape", [(1, 8, 8, 2048, 2048, 128, True), (2, 8, 2, 1000, 3000, 64, False),
                                    (1, 16, 4, 3000, 1000, 32, True)],
                          ids=lambda s: "B{}H{}K{}M{}N{}D{}{}".format(*s[:6], "c" if s[6] else "f"))
@@ -184,8 +234,9 @@ def test_total_attention_module_matches_forward(gpu):
     assert torch.equal(tot, t2)
 
 
-def test_attention_backward_metric_shape(gpu):
-    """B1 H32 S1024 D128 fp16 causal: gradients against the fp64 oracle."""
+def test_attention_backward_b1h32s1024(gpu):
+    """B1 H32 S1024 D128 fp16 causal (the metric shape's heads and head dim
+    at a quarter of its length): gradients against the fp64 oracle."""
     B, H, S, D = 1, 32, 1024, 128
     print("[case] attention backward B1 H32 S1024 D128 f16 causal", flush=True)
     q, k, v = inputs.make_qkv(B, H, H, S, S, D, dtype=torch.float16, seed=0)

@@ -137,3 +137,24 @@ def test_metric_shape_scores_properties(gpu):
                                   want=("out", "scores"))
     assert_out_close(o[:, 3:4], ref["out"])
     assert_scores_close(sc[:, 3:4], ref["scores"])
+
+
+def test_metric_shape_softmax_col_sum(gpu):
+    """The north star's MFMA target, attention_with_softmax_col_sum at
+    B1 H32 S4096 D128 fp16 causal (attention_with_col_softmax_sum.py:224-270):
+    three heads against the oracle, and for every head the column sums add up
+    to S (each of the S softmax rows sums to 1)."""
+    B, H, S, D = 1, 32, 4096, 128
+    print("[case] metric softmax col sum", flush=True)
+    q, k, v = inputs.make_qkv(B, H, H, S, S, D, dtype=torch.float16, seed=0)
+    qd, kd, vd = _dev(q, gpu), _dev(k, gpu), _dev(v, gpu)
+    o, col = fas.attention_with_softmax_col_sum(qd, kd, vd, causal=True)
+    torch.cuda.synchronize()
+    assert col.shape == (B, H, S) and col.dtype == torch.float32
+    tot = col.double().sum(-1).cpu()
+    assert torch.allclose(tot, torch.full_like(tot, S), rtol=1e-4)
+    for h in (0, 17, 31):
+        ref = naive.reference_forward(q[:, h:h + 1], k[:, h:h + 1], v[:, h:h + 1], causal=True,
+                                      want=("out", "col_softmax"))
+        assert_out_close(o[:, h:h + 1], ref["out"])
+        assert_sum_close(col[:, h:h + 1], ref["col_softmax"], f"col_softmax head {h}")

@@ -53,9 +53,18 @@ def _call_both(lib, shape, dtype, causal, gpu, seed):
 @pytest.mark.parametrize("first,second", [
     ((1, 8, 2, 1024, 1024, 128), (1, 4, 4, 300, 300, 64)),    # GQA then MHA, smaller
     ((2, 4, 2, 32, 4096, 128), (1, 2, 1, 16, 1000, 32)),      # key-split plans
+    # 128 row blocks of 256 against 64 key tiles: the allocating entry point
+    # splits each block's keys 4 ways (68.7 MB of partials, past the 64 MiB
+    # scratch); the no-allocation entry point must shrink the plan (3 splits).
+    ((1, 128, 128, 256, 4096, 128), (1, 4, 4, 300, 300, 64)),
 ])
 def test_noalloc_matches_allocating_entry_point(first, second, gpu):
     lib = _native.load()
+    if first[1] == 128:
+        q, k, v = (torch.empty((1, 128, n, 128), dtype=torch.float16) for n in (256, 4096, 4096))
+        a = _native.make_args(q, k, v, q, True, 128 ** -0.5)
+        full = lib.fas_workspace_bytes(_native.VARIANT_SOFTMAX_COL_SUM, ctypes.byref(a), 0)
+        assert full > 64 << 20, full
     _call_both(lib, first, torch.float16, True, gpu, seed=1)
     _call_both(lib, second, torch.bfloat16, True, gpu, seed=2)
 
