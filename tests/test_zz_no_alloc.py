@@ -71,12 +71,20 @@ def test_noalloc_matches_allocating_entry_point(first, second, gpu):
 
 def test_noalloc_rejects_oversized_problem(gpu):
     """B*Hq*M*4 bytes of row normalizers beyond 64 MiB: rejected before any
-    launch (no device memory is touched: the pointers are never read)."""
+    launch.  The arguments are otherwise valid (aligned, non-null addresses,
+    contiguous strides) so that the argument checks pass; no device memory is
+    touched, because the workspace check fails before any HIP call."""
     lib = _native.load()
     a = _native.AttnArgs()
     a.dtype, a.causal, a.sm_scale = 0, 1, 0.125
-    a.batch, a.heads_q, a.heads_k, a.seqlen_q, a.seqlen_k, a.head_dim = 64, 64, 64, 8192, 8192, 64
-    out = (ctypes.c_int64 * 3)(64 * 8192, 8192, 1)
-    rc = lib.fas_attention_with_softmax_col_sum_noalloc(ctypes.byref(a), None, out, None)
+    B, H, S, D = 64, 64, 8192, 64
+    a.batch, a.heads_q, a.heads_k, a.seqlen_q, a.seqlen_k, a.head_dim = B, H, H, S, S, D
+    fake = 1 << 40  # 256-byte aligned stand-in addresses, never dereferenced
+    a.q, a.k, a.v, a.out = fake, 2 * fake, 3 * fake, 4 * fake
+    for name in ("q_stride", "k_stride", "v_stride", "out_stride"):
+        setattr(a, name, (ctypes.c_int64 * 4)(H * S * D, S * D, D, 1))
+    out = (ctypes.c_int64 * 3)(H * S, S, 1)
+    rc = lib.fas_attention_with_softmax_col_sum_noalloc(ctypes.byref(a), ctypes.c_void_p(5 * fake),
+                                                        out, None)
     assert rc == _native.FAS_ERR_WORKSPACE
     assert "64" in _native.last_error(lib) and "scratch" in _native.last_error(lib)
