@@ -328,8 +328,50 @@ struct SplitPlan {
   int64_t mpad = 0;
 };
 
+// Head split of the softmax column pass (ColsmParams.fold / nsplit): one
+// workgroup per (unit, split, output group), a unit being a mirror pair of
+// 256-key blocks (colsm64_kernel) or one key block (the buffered pass).
+// With fold heads per output column, nsplit workgroups share a unit's heads
+// (heads s, s + nsplit, ...) and fold their column sums through partials and
+// a ticket per unit; nsplit is the smallest of least cost, cost = rounds of
+// `slots` concurrent workgroups x heads per workgroup, so a problem with few
+// output groups still fills the chip (B1 with 4 KV heads of 7 query heads:
+// 7 splits, 224 workgroups), and one that fills it walks all of a KV head's
+// query heads per workgroup with its keys resident (8 KV heads of 4 query
+// heads at 16K keys: 256 workgroups, no split).
+struct ColPlan {
+  int fold = 1, nsplit = 1;
+  int64_t nunits = 0, ngroups = 0;
+};
+constexpr int64_t kCus = 256;  // MI355X compute units
+ColPlan col_plan(const Problem& pr, bool buffered, int64_t ncols, bool fold_heads) {
+  ColPlan c;
+  c.fold = fold_heads ? pr.G : 1;
+  c.ngroups = (int64_t)pr.B * (pr.H / c.fold);
+  int64_t slots = kCus;  // colsm64_kernel: one 8-wave workgroup per CU
+  if (buffered) {
+    const int64_t bk = ncols % 4 == 0 ? 256 : 64;  // keys per workgroup (VEC or not)
+    c.nunits = (ncols + bk - 1) / bk;
+    slots = 8 * kCus;  // 4-wave workgroups, eight per CU
+  } else {
+    c.nunits = ((ncols + 255) / 256 + 1) / 2;
+  }
+  int64_t best = INT64_MAX;
+  for (int ns = 1; ns <= c.fold; ++ns) {
+    const int64_t wgs = c.nunits * ns * c.ngroups;
+    const int64_t cost = ((wgs + slots - 1) / slots) * ((c.fold + ns - 1) / ns);
+    if (cost < best) {
+      best = cost;
+      c.nsplit = ns;
+    }
+  }
+  return c;
+}
+
 struct Workspace {
   size_t lse = 0, part = 0, bsum = 0, region = 0, total = 0;  // byte offsets / total
+  size_t ticket = 0;                                            // column-pass tickets
+  ColPlan cp;                                                   // column-pass head split
   size_t bits = 0;                                              // dropout keep bits
   bool has_bits = false;
   size_t nl = 0, delta = 0;                                     // backward row values
@@ -494,10 +536,14 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
     w.has_lse = true;
     w.lse = off;
     off += align256((size_t)pr.B * pr.H * pr.M * 4);
-    if (pr.G > 1) {
+    w.cp = col_plan(pr, variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED, ncols, true);
+    if (w.cp.nsplit > 1) {
+      // The splits' column sums and one ticket per (output group, unit).
       w.has_part = true;
       w.part = off;
-      off += align256((size_t)pr.B * pr.H * ncols * 4);
+      off += align256((size_t)w.cp.ngroups * w.cp.nsplit * ncols * 4);
+      w.ticket = off;
+      off += align256((size_t)w.cp.ngroups * w.cp.nunits * 4);
     }
   }
   // The softmax column sum with dropout: the forward stores its keep
@@ -680,6 +726,11 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   fas::FwdParams p = fwd_params(a, pr, false, fas::kFwdRows);
   p.lse2 = at<float>(ws, w.lse);
   if (w.has_bits) p.drop_bits = at<uint32_t>(ws, w.bits);
+  if (w.cp.nsplit > 1) {
+    // The forward clears the column pass's tickets.
+    p.zero_words = at<uint32_t>(ws, w.ticket);
+    p.n_zero_words = (int)(w.cp.ngroups * w.cp.nunits);
+  }
   if (!buffered) apply_split(p, w, ws);
   if (buffered) {
     p.region = at<float>(ws, w.region);
@@ -714,23 +765,17 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   c.dropout = variant == FAS_VARIANT_SOFTMAX_COL_SUM && p.dropout ? (w.has_bits ? 2 : 1) : 0;
   c.drop = p.drop;
   c.drop_bits = p.drop_bits;
-  float* part = nullptr;
-  if (pr.G > 1) {
-    part = at<float>(ws, w.part);
-    c.out = part;
-    c.so0 = (int64_t)pr.H * ncols;
-    c.so1 = ncols;
-    c.so2 = 1;
-  } else {
-    c.out = out;
-    c.so0 = st[0]; c.so1 = st[1]; c.so2 = st[2];
+  c.out = out;
+  c.so0 = st[0]; c.so1 = st[1]; c.so2 = st[2];
+  // The column sums of a KV head's query heads, folded inside the pass.
+  c.fold = w.cp.fold;
+  c.nsplit = w.cp.nsplit;
+  if (w.cp.nsplit > 1) {
+    c.part = at<float>(ws, w.part);
+    c.ticket = at<uint32_t>(ws, w.ticket);
   }
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if ((rc = hip_status(fn, fas::launch_colsm(c, pr.dtype, pr.D, buffered, s)))) return rc;
-  if (pr.G > 1)
-    return hip_status(fn, fas::launch_group_reduce(part, out, st[0], st[1], st[2], pr.B, pr.Hk,
-                                                   pr.G, (int)ncols, s));
-  return FAS_OK;
+  return hip_status(fn, fas::launch_colsm(c, pr.dtype, pr.D, buffered,
+                                          static_cast<hipStream_t>(stream)));
 }
 
 // ------------------------------------------------- no-allocation scratch
@@ -1074,6 +1119,10 @@ int fas_total_attention(const fas_attn_args* a, const float* lse, const int64_t 
   c.causal_off = pr.N - pr.M;
   c.nkb = (pr.N + 255) / 256;
   c.qk_scale = qk_scale_of(pr.sm_scale);
+  // One output row per query head, no head split (no forward pass here to
+  // clear tickets).
+  c.fold = 1;
+  c.nsplit = 1;
   return hip_status(fn, fas::launch_colsm(c, pr.dtype, pr.D, false,
                                           static_cast<hipStream_t>(stream)));
 }

@@ -269,6 +269,8 @@ void fwd_kernel(const FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
   const bool loader = !kSplit || wave < NH;
+  if (blockIdx.x == 0 && p.zero_words != nullptr)
+    for (int i = tid; i < p.n_zero_words; i += NW * 64) p.zero_words[i] = 0u;
 
   // Split over keys: the plain and row-sum modes may give a row block to
   // nsplit workgroups, each over its own share of the key tiles.

@@ -15,8 +15,6 @@ constexpr int kFwdRows = 256;
 
 // Softmax-weight column sums after a forward pass that wrote lse2.
 hipError_t launch_colsm(const ColsmParams& p, int dtype, int d, bool buffered, hipStream_t s);
-hipError_t launch_group_reduce(const float* part, float* out, int64_t so0, int64_t so1,
-                               int64_t so2, int B, int Hk, int G, int ncols, hipStream_t s);
 // Raw-score column sums: block sums of q, suffix scan, per-key dot products.
 hipError_t launch_rawsum(const RawParams& p, int dtype, bool suffix, hipStream_t s);
 

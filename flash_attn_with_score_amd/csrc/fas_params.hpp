@@ -100,6 +100,10 @@ struct FwdParams {
   float* part_r;     // (B*H, nsplit, Mpad) raw row sums (kFwdRowSum)
   float sm_scale;    // |sm_scale|
   float qk_scale;    // |sm_scale| * log2(e)
+  // Words workgroup 0 sets to zero before anything else: the tickets of the
+  // column pass that follows on the same stream (ColsmParams.ticket).
+  uint32_t* zero_words;
+  int n_zero_words;
 };
 
 }  // namespace fas
@@ -114,13 +118,26 @@ struct ColsmParams {
   const float* lse_ln;   // or, when set, the natural-log normalizer (B,H,M) strided
   int64_t sl0, sl1, sl2;
   const float* region;   // buffered source: (B*H, M - split, split) raw fp32 scores
-  float* out;            // G == 1: (B, Hk, ncols) strided output; else partials (B*H, ncols)
+  float* out;            // (B, H / fold, ncols) strided output
   int64_t sq0, sq1, sq2;
   int64_t sk0, sk1, sk2;
-  int64_t so0, so1, so2;  // output strides (G == 1) or (H*ncols, ncols, 1)
+  int64_t so0, so1, so2;
   uint32_t q_bytes, k_bytes;
   uint32_t qneg;
   int B, H, G, M, N;
+  // Head folding: output column group og = b * (H / fold) + ho sums the
+  // query heads ho*fold .. ho*fold + fold - 1 (fold = G: the column sums per
+  // KV head; fold = 1: per query head, total_attention).  The fold's heads
+  // are dealt to nsplit workgroups per key block (pair), split s taking
+  // heads s, s + nsplit, ...; with nsplit > 1 each writes its column sums to
+  // part[(og * nsplit + s) * ncols + key] and bumps ticket[og * nunits +
+  // unit] (unit = the key block or pair), and the workgroup that brings the
+  // ticket to nsplit adds the nsplit partials in split order into out.
+  // The tickets start at 0: the forward pass of the same call clears them
+  // (FwdParams.zero_words).
+  int fold, nsplit;
+  float* part;
+  uint32_t* ticket;
   int row_lo;            // first query row that contributes (0, or split)
   int ncols;             // keys summed: N, or split
   int split;             // region row offset / pitch (buffered)

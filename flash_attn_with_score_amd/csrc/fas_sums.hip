@@ -6,8 +6,8 @@ namespace fas {
 
 template <class E, int D>
 static hipError_t colsm_t(const ColsmParams& p, hipStream_t s) {
-  // One workgroup per mirror pair of key blocks.
-  const dim3 grid((unsigned)((int64_t)((p.nkb + 1) / 2) * p.B * p.H));
+  // One workgroup per mirror pair of key blocks, head split and output group.
+  const dim3 grid((unsigned)((int64_t)((p.nkb + 1) / 2) * p.nsplit * p.B * (p.H / p.fold)));
   if (p.lse_ln != nullptr)
     hipLaunchKernelGGL((colsm64_kernel<E, D, true, 0>), grid, dim3(512), 0, s, p);
   else if (p.dropout == 2)
@@ -26,7 +26,7 @@ hipError_t launch_colsm(const ColsmParams& p, int dtype, int d, bool buffered, h
     const int64_t nkb = (p.ncols + (vec ? 255 : 63)) / (vec ? 256 : 64);
     ColsmParams q = p;
     q.nkb = (int)nkb;
-    const dim3 grid((unsigned)(nkb * p.B * p.H));
+    const dim3 grid((unsigned)(nkb * p.nsplit * p.B * (p.H / p.fold)));
     if (vec)
       hipLaunchKernelGGL(colsm_buffered_kernel<true>, grid, dim3(256), 0, s, q);
     else
@@ -49,17 +49,6 @@ hipError_t launch_colsm(const ColsmParams& p, int dtype, int d, bool buffered, h
     }
   }
   return hipErrorInvalidValue;
-}
-
-hipError_t launch_group_reduce(const float* part, float* out, int64_t so0, int64_t so1,
-                               int64_t so2, int B, int Hk, int G, int ncols, hipStream_t s) {
-  const int64_t total = (int64_t)B * Hk * ncols;
-  if (total <= 0) return hipSuccess;
-  int64_t blocks = (total + 255) / 256;
-  if (blocks > 8192) blocks = 8192;
-  hipLaunchKernelGGL(group_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, part, out, so0,
-                     so1, so2, B, Hk, G, ncols);
-  return hipGetLastError();
 }
 
 template <class E, int D>

@@ -9,7 +9,10 @@
 // (the forward pass's final base-2 log-sum-exp) is summed over queries
 // in-lane.  Every column is owned by one workgroup: no atomics, the result is
 // deterministic.
-// GQA groups are folded afterwards by group_reduce_kernel in a fixed order.
+// GQA groups are folded inside the pass: a workgroup walks the query heads
+// of its KV head with its keys resident, or, when that would leave CUs idle,
+// shares them with other workgroups and the last one to finish adds their
+// column sums in a fixed order.
 //
 // Raw-score column sums (attention_with_col_sum.py:186-191,
 // attention_with_col_sum_sequential.py:177-182,
@@ -32,17 +35,81 @@ constexpr uint32_t kOffNoneSums = 0x80000000u;
 
 // ---------------------------------------------------------------- softmax
 
-__device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb, int& bh) {
-  // Same XCD-aware dealing as the forward kernel; key blocks ascending, which
-  // for causal masks is longest first.
-  if ((BH & 7) == 0) {
-    const int x = bid & 7, s = bid >> 3, per = BH >> 3;
-    bh = x * per + s % per;
-    kb = s / per;
-  } else {
-    bh = bid % BH;
-    kb = bid / BH;
-  }
+// Workgroup bid runs on XCD bid % 8.  Work items [0, T) are dealt to the
+// XCDs in contiguous runs: XCD x takes ceil((T - x) / 8) of them, so items
+// that read the same rows of q or k (neighbours in item order) share an L2.
+__device__ __forceinline__ int xcd_item(int bid, int T) {
+  const int x = bid & 7, s = bid >> 3;
+  return x * (T >> 3) + min(x, T & 7) + s;
+}
+
+// Column-pass work item: unit u of the nunits per output group (a key block
+// or a mirror pair of them), head split sp, output group og; item order
+// (og, sp, u), u fastest, so the units reading one split's q rows are
+// neighbours.
+struct ColItem {
+  int unit, sp, og;
+};
+__device__ __forceinline__ ColItem col_item(int bid, int nunits, int nsplit, int nog) {
+  const int item = xcd_item(bid, nunits * nsplit * nog);
+  ColItem c;
+  c.unit = item % nunits;
+  const int rest = item / nunits;
+  c.sp = rest % nsplit;
+  c.og = rest / nsplit;
+  return c;
+}
+
+// With a head split (p.nsplit > 1) the splits of a unit run on other XCDs,
+// whose L2 caches are not coherent with this one's, so their column sums
+// meet at device scope: each split stores them with device-scope (relaxed
+// atomic) stores, which write through to the device's coherent level, and
+// waits for them to complete; one thread then takes the unit's ticket (a
+// device-scope atomic), and the workgroup that takes the last one reads the
+// nsplit partials of keys [kA0, kA1) and [kB0, kB1) with device-scope loads
+// and adds them in split order.  Fences would write back and invalidate the
+// whole L2 at every workgroup's end instead (measured: config-3 column pass
+// 75 -> 108 us).
+__device__ __forceinline__ void store_part(const ColsmParams& p, const ColItem& it, int key,
+                                           float v) {
+  __hip_atomic_store(&p.part[((int64_t)it.og * p.nsplit + it.sp) * p.ncols + key], v,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void col_fold_splits(const ColsmParams& p, const ColItem& it,
+                                                int nunits, int kA0, int kA1, int kB0, int kB1,
+                                                bool* last_flag) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *last_flag = __hip_atomic_fetch_add(&p.ticket[(int64_t)it.og * nunits + it.unit], 1u,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(p.nsplit - 1);
+  __syncthreads();
+  if (!*last_flag) return;
+  const int hout = p.H / p.fold;
+  const int b = it.og / hout, ho = it.og - b * hout;
+  float* src = p.part + (int64_t)it.og * p.nsplit * p.ncols;
+  auto fold_range = [&](int k0, int k1) {
+    for (int key = k0 + (int)threadIdx.x; key < k1; key += (int)blockDim.x) {
+      // Eight loads in flight at a time (they miss the L2), added in split
+      // order; splits past nsplit add 0.
+      float acc = 0.f;
+      for (int s0 = 0; s0 < p.nsplit; s0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = s0 + i < p.nsplit
+                     ? __hip_atomic_load(&src[(int64_t)(s0 + i) * p.ncols + key],
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                     : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += v[i];
+      }
+      p.out[b * p.so0 + ho * p.so1 + (int64_t)key * p.so2] = acc;
+    }
+  };
+  fold_range(kA0, kA1);
+  fold_range(kB0, kB1);
 }
 
 // The column pass with 64 keys per wave.  Each 32x16 Q operand fetched from
@@ -65,6 +132,13 @@ __device__ __forceinline__ void map_block_keys(int bid, int nkb, int BH, int& kb
 // next block's MFMAs, or streaming Q by LDS DMA in 256-row steps, left the
 // time unchanged: at the board's power limit the energy of this work, not
 // its issue order, bounds the pass.
+// GQA (attention_with_col_softmax_sum.py:61-67, 264-270 add every query
+// head of a KV head into one column): the workgroup walks the query heads
+// of its split one after the other with its keys resident in VGPRs, the
+// column sums accumulating over all of them in registers; the row steps of
+// consecutive heads form one pipeline (the next head's first rows are
+// fetched during the current head's last step).  K is therefore read once
+// per workgroup, not once per query head.
 // LN: the row offsets come from a natural-log normalizer (p.lse_ln,
 // total_attention) instead of the forward's base-2 LSE; a template flag so
 // the default copy carries no conversion code in its loop.
@@ -93,31 +167,32 @@ void colsm64_kernel(const ColsmParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t qlds[2][TQ * D];
   __shared__ __attribute__((aligned(16))) float llds[2][TQ];
   __shared__ float red[4][64];
+  __shared__ bool last_flag;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
   const int kg = wave & 3, rg = wave >> 2;
   const int npairs = (p.nkb + 1) / 2;
-  int pb, bh;
-  map_block_keys(blockIdx.x, npairs, p.B * p.H, pb, bh);
-  const int h = bh % p.H, b = bh / p.H, hk = h / p.G;
+  const int hout = p.H / p.fold;
+  const ColItem item = col_item(blockIdx.x, npairs, p.nsplit, p.B * hout);
+  const int pb = item.unit;
+  const int b = item.og / hout, ho = item.og - b * hout;
+  const int hfirst = ho * p.fold;   // first query head of the output group
+  const int hk = hfirst / p.G;
+  // Heads of this split: hfirst + j, j = sp, sp + nsplit, ... < fold.
+  const int nheads = (p.fold - item.sp + p.nsplit - 1) / p.nsplit;
   const int kbb = p.nkb - 1 - pb;
 
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
-  const float* lse = p.lse2 + (int64_t)bh * p.M;
   const int t1 = (p.M + TQ - 1) / TQ;
-  __amdgpu_buffer_rsrc_t rbits = make_rsrc(p.drop_bits, 0);
-  if constexpr (DROP == 2) {
-    const int r32 = (p.M + 31) >> 5;
-    rbits = make_rsrc(p.drop_bits + (int64_t)bh * r32 * p.N,
-                      __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)r32 * p.N * 4)));
-  }
+  const int r32 = (p.M + 31) >> 5;
 
   u32x4 qst[CPT];
   float lst = 0.f;
-  auto fetch = [&](int t) {
+  // Q rows and row offsets of step t of head h.
+  auto fetch = [&](int h, int t) {
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int id = tid + i * NT;
@@ -129,7 +204,7 @@ void colsm64_kernel(const ColsmParams p) {
       if (row < p.row_lo || row >= p.M) {
         lst = pos_inf();
       } else if constexpr (!LN) {
-        lst = lse[row];
+        lst = p.lse2[(int64_t)(b * p.H + h) * p.M + row];
       } else {
         // total_attention(): the caller's natural-log normalizer, -inf for
         // rows that see no key (total.py:125-128).
@@ -153,9 +228,17 @@ void colsm64_kernel(const ColsmParams p) {
     if (tid < TQ) llds[stage][tid] = -lst * inv_scale;
   };
 
+  int kA0 = 0, kA1 = 0, kB0 = 0, kB1 = 0;  // key ranges of the two blocks
   for (int blk = 0; blk < 2; ++blk) {
     const int kb = blk == 0 ? pb : kbb;
     if (blk == 1 && kbb == pb) break;
+    if (blk == 0) {
+      kA0 = kb * BK;
+      kA1 = min(p.ncols, kA0 + BK);
+    } else {
+      kB0 = kb * BK;
+      kB1 = min(p.ncols, kB0 + BK);
+    }
     // Keys of this wave: [key0, key0 + 64), set j = keys key0 + 32 j + c.
     const int key0 = kb * BK + 64 * kg;
     u32x4 kreg[2][KS];
@@ -176,13 +259,18 @@ void colsm64_kernel(const ColsmParams p) {
     int rstart = p.row_lo;
     if (p.causal) rstart = max(rstart, kb * BK - p.causal_off);
     const int t0 = max(0, rstart) / TQ;
+    const int nt = t1 > t0 ? t1 - t0 : 0;
+    const int nsteps = nheads * nt;  // (head, step) pairs, head-major
 
     float colacc[2] = {0.f, 0.f};
-    // Keep words of step t (DROP == 2): block (qb, j) is rows
+    // Keep words of step t of head h (DROP == 2): block (qb, j) is rows
     // t*TQ + 64 rg + 32 qb .. +31 of key key0 + 32 j + c.
     uint32_t bcur[4] = {0u, 0u, 0u, 0u}, bnext[4] = {0u, 0u, 0u, 0u};
-    auto fetch_bits = [&](int t, uint32_t (&w)[4]) __attribute__((always_inline)) {
+    auto fetch_bits = [&](int h, int t, uint32_t (&w)[4]) __attribute__((always_inline)) {
       if constexpr (DROP == 2) {
+        const __amdgpu_buffer_rsrc_t rbits =
+            make_rsrc(p.drop_bits + (int64_t)(b * p.H + h) * r32 * p.N,
+                      __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)r32 * p.N * 4)));
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
@@ -194,19 +282,31 @@ void colsm64_kernel(const ColsmParams p) {
           }
       }
     };
-    if (t0 < t1) {
-      fetch(t0);
-      fetch_bits(t0, bcur);
+    // The step being computed (head ch, row step ct) and the one after it.
+    int ch = hfirst + item.sp, ct = t0;
+    auto advance = [&](int& h, int& t) __attribute__((always_inline)) {
+      if (++t == t1) {
+        t = t0;
+        h += p.nsplit;
+      }
+    };
+    if (nsteps > 0) {
+      fetch(ch, ct);
+      fetch_bits(ch, ct, bcur);
       stash(0);
     }
     __syncthreads();
-    auto step = [&](int t, auto stage_tag) __attribute__((always_inline)) {
+    auto step = [&](int i, auto stage_tag) __attribute__((always_inline)) {
       constexpr int stage = decltype(stage_tag)::value;
-      const bool more = t + 1 < t1;
+      const bool more = i + 1 < nsteps;
+      int nh = ch, ntt = ct;
+      advance(nh, ntt);
       if (more) {
-        fetch(t + 1);
-        fetch_bits(t + 1, bnext);
+        fetch(nh, ntt);
+        fetch_bits(nh, ntt, bnext);
       }
+      const int t = ct;
+      const uint32_t bh = (uint32_t)(b * p.H + ch);
       const int r0 = t * TQ + 64 * rg;  // this row group's first row
       const uint16_t* qt = qlds[stage];
 #pragma unroll
@@ -248,9 +348,9 @@ void colsm64_kernel(const ColsmParams p) {
             constexpr int PD = KS < 2 ? KS : 2;
             __builtin_amdgcn_sched_group_barrier(0x100, PD + 4, 0);  // DS read: 4 of -lse, PD of Q
 #pragma unroll
-            for (int i = 0; i < KS; ++i) {
+            for (int i2 = 0; i2 < KS; ++i2) {
               __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-              if (i + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+              if (i2 + PD < KS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
           }
 #pragma unroll
@@ -264,7 +364,7 @@ void colsm64_kernel(const ColsmParams p) {
               }
               if constexpr (DROP == 1) {
                 const uint32_t row = (uint32_t)(rq0 + acc_row(r, g));
-                const uint32_t idx = ((uint32_t)bh * (uint32_t)p.M + row) * (uint32_t)p.drop.n +
+                const uint32_t idx = (bh * (uint32_t)p.M + row) * (uint32_t)p.drop.n +
                                      (uint32_t)(key0 + 32 * j + c);
                 if (!dropout_keep(p.drop, idx)) s[j][r] = 0.f;
               }
@@ -294,13 +394,15 @@ void colsm64_kernel(const ColsmParams p) {
       if (more) {
         stash(stage ^ 1);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bcur[i] = bnext[i];
+        for (int k = 0; k < 4; ++k) bcur[k] = bnext[k];
       }
+      ch = nh;
+      ct = ntt;
       __syncthreads();
     };
-    for (int t = t0; t < t1; t += 2) {
-      step(t, std::integral_constant<int, 0>{});
-      if (t + 1 < t1) step(t + 1, std::integral_constant<int, 1>{});
+    for (int i = 0; i < nsteps; i += 2) {
+      step(i, std::integral_constant<int, 0>{});
+      if (i + 1 < nsteps) step(i + 1, std::integral_constant<int, 1>{});
     }
     // Fold the half-waves, then row group 1 into row group 0 (fixed order).
     float tot[2];
@@ -315,22 +417,29 @@ void colsm64_kernel(const ColsmParams p) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int key = key0 + 32 * j + c;
-        if (key < p.ncols)
-          p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] = tot[j] + red[kg][32 * j + c];
+        if (key < p.ncols) {
+          const float v = tot[j] + red[kg][32 * j + c];
+          if (p.nsplit == 1)
+            p.out[b * p.so0 + ho * p.so1 + (int64_t)key * p.so2] = v;
+          else
+            store_part(p, item, key, v);
+        }
       }
     }
     __syncthreads();
   }
+  if (p.nsplit > 1) col_fold_splits(p, item, npairs, kA0, kA1, kB0, kB1, &last_flag);
 }
 #pragma clang diagnostic pop
 
 // Buffered source: pass 1 left the raw fp32 scores of the region (rows >=
 // split, keys < split; masked entries -inf) in p.region.  A workgroup of 4
-// waves owns 256 keys of one (b, h): lane l of every wave holds keys
-// 4 l .. 4 l + 3 and reads them as one 16-byte load per row, so a wave reads
-// 1 KiB contiguous per row; the waves take every fourth row (the row and its
-// lse2 are wave-uniform, the latter a scalar load), several rows in flight,
-// and their sums meet in LDS in a fixed order.  Entries above a key's first
+// waves owns 256 keys of one output group and walks the query heads of its
+// split one after the other: lane l of every wave holds keys 4 l .. 4 l + 3
+// and reads them as one 16-byte load per row, so a wave reads 1 KiB
+// contiguous per row; the waves take every fourth row (the row and its lse2
+// are wave-uniform, the latter a scalar load), several rows in flight, and
+// their sums meet in LDS in a fixed order.  Entries above a key's first
 // admissible row were never written and are excluded by a select.  VEC:
 // split % 4 == 0 (16-byte aligned rows); otherwise one key per lane.
 template <bool VEC>
@@ -338,15 +447,15 @@ __global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p
   constexpr int KPL = VEC ? 4 : 1;  // keys per lane
   constexpr int BKB = 64 * KPL;     // keys per workgroup
   __shared__ float red[4][256];
-  int kb, bh;
-  map_block_keys(blockIdx.x, p.nkb, p.B * p.H, kb, bh);
-  const int h = bh % p.H, b = bh / p.H;
+  __shared__ bool last_flag;
+  const int hout = p.H / p.fold;
+  const ColItem item = col_item(blockIdx.x, p.nkb, p.nsplit, p.B * hout);
+  const int kb = item.unit;
+  const int b = item.og / hout, ho = item.og - b * hout;
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int key0 = kb * BKB + KPL * lane;
   const int rows = max(0, p.M - p.split);
-  const float* reg = p.region + (int64_t)bh * rows * p.split;
-  const float* lse = p.lse2 + (int64_t)bh * p.M;
   // First admissible row of each key, and of the workgroup's first key.
   int rs[KPL];
 #pragma unroll
@@ -356,57 +465,51 @@ __global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p
   float acc[KPL];
 #pragma unroll
   for (int e = 0; e < KPL; ++e) acc[e] = 0.f;
-  auto row_step = [&](int row) __attribute__((always_inline)) {
-    const float l = lse[row];
-    const float* rp = reg + (int64_t)(row - p.split) * p.split + key0;
-    float v[KPL];
-    if constexpr (VEC) {
-      const f32x4 x = live ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rp))
-                           : f32x4{0.f, 0.f, 0.f, 0.f};
-      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-    } else {
-      v[0] = live ? rp[0] : 0.f;
-    }
+  for (int h = ho * p.fold + item.sp; h < (ho + 1) * p.fold; h += p.nsplit) {
+    const int64_t bh = (int64_t)b * p.H + h;
+    const float* reg = p.region + bh * rows * p.split;
+    const float* lse = p.lse2 + bh * p.M;
+    auto row_step = [&](int row) __attribute__((always_inline)) {
+      const float l = lse[row];
+      const float* rp = reg + (int64_t)(row - p.split) * p.split + key0;
+      float v[KPL];
+      if constexpr (VEC) {
+        const f32x4 x = live ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rp))
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      } else {
+        v[0] = live ? rp[0] : 0.f;
+      }
 #pragma unroll
-    for (int e = 0; e < KPL; ++e) {
-      const float w = exp2f_fast(fmaf(v[e], p.qk_scale, -l));
-      acc[e] += row >= rs[e] ? w : 0.f;
-    }
-  };
-  int row = __builtin_amdgcn_readfirstlane(r_lo + wave);
+      for (int e = 0; e < KPL; ++e) {
+        const float w = exp2f_fast(fmaf(v[e], p.qk_scale, -l));
+        acc[e] += row >= rs[e] ? w : 0.f;
+      }
+    };
+    int row = __builtin_amdgcn_readfirstlane(r_lo + wave);
 #pragma unroll 1
-  for (; row + 12 < p.M; row += 16) {
-    row_step(row);
-    row_step(row + 4);
-    row_step(row + 8);
-    row_step(row + 12);
+    for (; row + 12 < p.M; row += 16) {
+      row_step(row);
+      row_step(row + 4);
+      row_step(row + 8);
+      row_step(row + 12);
+    }
+    for (; row < p.M; row += 4) row_step(row);
   }
-  for (; row < p.M; row += 4) row_step(row);
 #pragma unroll
   for (int e = 0; e < KPL; ++e) red[wave][KPL * lane + e] = acc[e];
   __syncthreads();
   const int t = threadIdx.x;
   const int key = kb * BKB + t;
-  if (t < BKB && key < p.ncols)
-    p.out[b * p.so0 + h * p.so1 + (int64_t)key * p.so2] =
-        (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
-}
-
-// out[b, hk, j] = sum over the G query heads of group hk of part[b*H + h, j],
-// heads added in increasing order.
-__global__ void group_reduce_kernel(const float* __restrict__ part, float* out, int64_t so0,
-                                    int64_t so1, int64_t so2, int B, int Hk, int G, int ncols) {
-  const int64_t total = (int64_t)B * Hk * ncols;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int j = (int)(i % ncols);
-    const int64_t bhk = i / ncols;
-    const int hk = (int)(bhk % Hk), b = (int)(bhk / Hk);
-    const float* src = part + ((int64_t)b * Hk * G + (int64_t)hk * G) * ncols + j;
-    float acc = 0.f;
-    for (int gg = 0; gg < G; ++gg) acc += src[(int64_t)gg * ncols];
-    out[b * so0 + hk * so1 + (int64_t)j * so2] = acc;
+  if (t < BKB && key < p.ncols) {
+    const float v = (red[0][t] + red[1][t]) + (red[2][t] + red[3][t]);
+    if (p.nsplit == 1)
+      p.out[b * p.so0 + ho * p.so1 + (int64_t)key * p.so2] = v;
+    else
+      store_part(p, item, key, v);
   }
+  if (p.nsplit > 1)
+    col_fold_splits(p, item, p.nkb, kb * BKB, min(p.ncols, kb * BKB + BKB), 0, 0, &last_flag);
 }
 
 // ---------------------------------------------------------------- raw sums

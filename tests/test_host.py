@@ -94,11 +94,45 @@ def make_args(B=1, Hq=4, Hk=2, M=300, N=300, D=128, causal=1, dtype=0, ptr=0x100
     return a
 
 
+def _col_plan(B, Hq, Hk, ncols, buffered, cus=256):
+    """Head split of the softmax column pass, restated: the fold's G query
+    heads are dealt to nsplit workgroups per unit (a mirror pair of 256-key
+    blocks, or one key block of the buffered pass); nsplit is the smallest of
+    least cost, cost = rounds of concurrent workgroups x heads per workgroup.
+    Returns (nsplit, units, output groups)."""
+    G = Hq // Hk
+    groups = B * Hk
+    if buffered:
+        bk = 256 if ncols % 4 == 0 else 64
+        units, slots = -(-ncols // bk), 8 * cus
+    else:
+        units, slots = (-(-ncols // 256) + 1) // 2, cus
+    cost = {ns: -(-(units * ns * groups) // slots) * -(-G // ns) for ns in range(1, G + 1)}
+    best = min(cost.values())
+    return min(ns for ns, c in cost.items() if c == best), units, groups
+
+
+def test_col_plan_examples():
+    """The plan on the BASELINE shapes: 7 splits for 4 KV heads of 7 query
+    heads (224 workgroups instead of 32), none at 8 KV heads x 32 pairs (256
+    workgroups), one head per workgroup for the cross-token pass at split
+    12288 (768 workgroups in 3 rounds beat 192 in one round of 4 heads)."""
+    assert _col_plan(1, 28, 4, 4096, False) == (7, 8, 4)
+    assert _col_plan(1, 32, 8, 16384, False) == (1, 32, 8)
+    assert _col_plan(1, 32, 8, 12288, False) == (4, 24, 8)
+    assert _col_plan(1, 32, 32, 4096, False) == (1, 8, 32)
+    assert _col_plan(1, 32, 8, 12288, True) == (4, 48, 8)
+
+
 def test_workspace_sizes(lib):
     B, Hq, Hk, M, N, D, split = 2, 8, 2, 300, 300, 64, 100
 
     def r256(x):
         return (x + 255) // 256 * 256
+
+    def folds(ncols, buffered):
+        ns, units, groups = _col_plan(B, Hq, Hk, ncols, buffered)
+        return 0 if ns == 1 else r256(groups * ns * ncols * 4) + r256(groups * units * 4)
 
     a = make_args(B, Hq, Hk, M, N, D)
     ws = lambda v: lib.fas_workspace_bytes(v, ctypes.byref(a), split)  # noqa: E731
@@ -107,11 +141,12 @@ def test_workspace_sizes(lib):
     nblk = (M + 63) // 64
     assert ws(_native.VARIANT_COL_SUM) == r256(B * Hk * (nblk + 1) * D * 4)
     assert ws(_native.VARIANT_COL_SUM_SEQUENTIAL) == ws(_native.VARIANT_COL_SUM)
-    assert ws(_native.VARIANT_SOFTMAX_COL_SUM) == r256(B * Hq * M * 4) + r256(B * Hq * N * 4)
+    assert folds(N, False) > 0  # 4 query heads per KV head, 4 workgroups unsplit: split
+    assert ws(_native.VARIANT_SOFTMAX_COL_SUM) == r256(B * Hq * M * 4) + folds(N, False)
     assert ws(_native.VARIANT_CROSS_QK_SUM) == r256(B * Hk * ((M - split + 63) // 64 + 1) * D * 4)
-    assert ws(_native.VARIANT_CROSS_SOFTMAX_SUM) == r256(B * Hq * M * 4) + r256(B * Hq * split * 4)
+    assert ws(_native.VARIANT_CROSS_SOFTMAX_SUM) == r256(B * Hq * M * 4) + folds(split, False)
     assert ws(_native.VARIANT_CROSS_SOFTMAX_SUM_BUFFERED) == (
-        r256(B * Hq * M * 4) + r256(B * Hq * split * 4) + r256(B * Hq * (M - split) * split * 4))
+        r256(B * Hq * M * 4) + folds(split, True) + r256(B * Hq * (M - split) * split * 4))
     # MHA needs no per-query-head partials.
     a1 = make_args(B, 4, 4, M, N, D)
     assert lib.fas_workspace_bytes(_native.VARIANT_SOFTMAX_COL_SUM, ctypes.byref(a1), 0) == \
@@ -208,8 +243,10 @@ def test_key_split_workspace(lib):
     ws = lambda v, s=0: lib.fas_workspace_bytes(v, ctypes.byref(a), s)  # noqa: E731
     assert ws(_native.VARIANT_ROW_SUM) == split
     assert ws(_native.VARIANT_ATTENTION_FORWARD) == split
+    ns, units, groups = _col_plan(B, Hq, Hk, N, False)
+    assert ns == 2
     assert ws(_native.VARIANT_SOFTMAX_COL_SUM) == (
-        r256(B * Hq * M * 4) + r256(B * Hq * N * 4) + split)
+        r256(B * Hq * M * 4) + r256(groups * ns * N * 4) + r256(groups * units * 4) + split)
     assert ws(_native.VARIANT_SCORES) == split  # key-split forward + scores-only kernel
     # enough row blocks: no split
     a = make_args(1, 32, 32, 4096, 4096, 128)
