@@ -943,20 +943,32 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
   // rounds the mirror order balances (B1 H32 S1024: 45.7 -> 37.5 us; H16
   // S4096: 179 -> 145 us; H32 S2048: 94.3 -> 95.9 us).
   // (The dropout instances exist with 256-row blocks only.)
+  const int vec_scores =
+      aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && pr.N % 8 == 0;
+  const int64_t cus = device_cu_count();
   if (pw.pack == 1 && !(a->dropout_p > 0.f) &&
-      (int64_t)pr.B * pr.H * ((pr.M + fas::kFwdRows - 1) / fas::kFwdRows) <= device_cu_count())
+      (int64_t)pr.B * pr.H * ((pr.M + fas::kFwdRows - 1) / fas::kFwdRows) <= cus) {
     bm = fas::kFwdRows / 2;
+    // When even the 128-row blocks all run in one round under a causal mask
+    // with long rows, the writer takes 64-row blocks with each block's key
+    // tiles split between its two wave pairs (16-byte score rows only): two
+    // rounds of balanced pairs.  A step of it moves twice the K/V bytes per
+    // score, so it pays only when the longest row block is long (measured:
+    // B1 H8 S4096 0.118 -> 0.096 ms; B1 H32 S1024 0.0367 -> 0.0383 ms).
+    if (vec_scores && pr.causal && pr.N >= 2048 &&
+        (int64_t)pr.B * pr.H * ((pr.M + bm - 1) / bm) <= cus)
+      bm = fas::kFwdRows / 4;
+  }
   fas::FwdParams p = fwd_params(a, pw, false, bm);
   rescale_dropout(p, a);
   p.scores = static_cast<uint16_t*>(scores);
   p.ss0 = st[0];
   p.ss1 = st[1];
   p.ss2 = st[2];
-  p.vec_scores =
-      aligned16(scores) && st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && pr.N % 8 == 0;
+  p.vec_scores = vec_scores;
   // The writer runs one workgroup per CU; with no more workgroups than CUs
   // they all run at once and each writes its own zero triangle.
-  p.zero_self = (int64_t)p.nrb * (pr.B * pr.H / pw.pack) <= device_cu_count() ? 1 : 0;
+  p.zero_self = (int64_t)p.nrb * (pr.B * pr.H / pw.pack) <= cus ? 1 : 0;
   return run_fwd(fn, p, pr, fas::kFwdScores, stream);
 }
 

@@ -230,15 +230,26 @@ __device__ __forceinline__ void sched_score_tile() {
 // per-lane head offset folds away at compile time.
 // Two waves per SIMD, except for the 4-wave score writer, whose LDS (one
 // workgroup per CU) allows one.
-template <class E, int D, int MODE, int NW, bool DROP, bool PACK>
+// KS2 (4-wave score writer only): 64-row blocks whose key range is split
+// between the wave pairs: loader wave i takes the even key tiles and storer
+// wave 2 + i the odd ones of the same 32 rows, so a step stages two key
+// tiles; at the end each storer hands its partial O, offset and weight sum
+// to its loader through LDS.  For problems whose 128-row blocks all run in
+// one round, where the longest causal row block alone set the kernel time:
+// 64-row blocks run in two rounds whose longest-first pairs (rb, 15 - rb)
+// all take the same number of steps.
+template <class E, int D, int MODE, int NW, bool DROP, bool PACK, bool KS2 = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 1 : 2, 2)))
 void fwd_kernel(const FwdParams p) {
   static_assert(MODE != kFwdScores || NW == 8 || NW == 4, "the score writer uses 4 or 8 waves");
+  static_assert(!KS2 || (MODE == kFwdScores && NW == 4 && !DROP && !PACK),
+                "the key-split writer is the unpacked 4-wave score writer");
   constexpr int NH = NW / 2;  // score writer: loader waves [0, NH), storer waves [NH, NW)
   const int pack = PACK ? p.pack : 1;
   constexpr int KS = D / 16;               // MFMA k-steps over the head dim
   constexpr int DB = (D + 31) / 32;        // 32-dim blocks of O^T
-  constexpr int BM = 32 * NW;
+  constexpr int BM = KS2 ? 32 * NH : 32 * NW;
+  constexpr int NTS = KS2 ? 2 : 1;         // key tiles per step (per LDS stage)
   constexpr int BN = 64;
   constexpr int TILE = BN * D;             // elements per K or V tile
   constexpr int BLOCKS = TILE / 512;       // 1 KiB DMA blocks per tile
@@ -255,7 +266,7 @@ void fwd_kernel(const FwdParams p) {
   // Zero-store slots per key tile and storer (issued during O += P V).
   constexpr int kZero = 8;  // zero stores per key tile: one ZeroRuns batch
 
-  __shared__ __attribute__((aligned(16))) uint16_t kv[2][2][TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t kv[2][NTS][2][TILE];
   __shared__ __attribute__((aligned(16))) u32x4 stg[SG];
   // Region tiles (kFwdRegion) leave through LDS too: a wave's 32 x 64 fp32
   // tile (8 KiB, 16-byte chunks XOR-swizzled by row) is read back row-major,
@@ -269,6 +280,9 @@ void fwd_kernel(const FwdParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
   const bool loader = !kSplit || wave < NH;
+  // The wave's 32-row slice of the row block, and (KS2) its key-tile parity.
+  const int slice = KS2 ? (wave & (NH - 1)) : wave;
+  const int kpar = KS2 && !loader ? 1 : 0;
   if (blockIdx.x == 0 && p.zero_words != nullptr)
     for (int i = tid; i < p.n_zero_words; i += NW * 64) p.zero_words[i] = 0u;
 
@@ -290,7 +304,7 @@ void fwd_kernel(const FwdParams p) {
   const int gpb = p.H / pack;  // groups per batch entry
   const int b = grp / gpb, h0 = (grp - b * gpb) * pack, hk = h0 / p.G;
   const int row0 = rb * BM;
-  const int wrow0 = row0 + 32 * wave;
+  const int wrow0 = row0 + 32 * slice;
   const int vrow = wrow0 + c;
   const int qpos = vrow / pack;
   const int qh = h0 + (vrow - qpos * pack);
@@ -303,7 +317,7 @@ void fwd_kernel(const FwdParams p) {
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h0 * p.sq1, p.q_bytes);
   const i32x4 wk = make_rsrc_words(p.k + b * p.sk0 + hk * p.sk1, p.k_bytes);
   const i32x4 wv = make_rsrc_words(p.v + b * p.sv0 + hk * p.sv1, p.v_bytes);
-  const uint32_t kv_base = lds_addr(&kv[0][0][0]);
+  const uint32_t kv_base = lds_addr(&kv[0][0][0][0]);
   // Byte offsets of the lane's q and out rows (kOffNone past M: q reads
   // zeros, out stores are dropped).
   const uint32_t qoff = row_ok ? (uint32_t)(((int64_t)(qh - h0) * p.sq1 + (int64_t)qpos * p.sq2) * 2)
@@ -323,7 +337,8 @@ void fwd_kernel(const FwdParams p) {
   const int ntiles = (hi + BN - 1) / BN;
   // This workgroup's key tiles [t_begin, t_end): all of them, or one split's
   // share (possibly none).
-  int t_begin = 0, t_end = ntiles;
+  // Loop steps [t_begin, t_end): one key tile each, or (KS2) two.
+  int t_begin = 0, t_end = KS2 ? (ntiles + 1) / 2 : ntiles;
   if constexpr (kCanSplit) {
     if (p.nsplit > 1) {
       t_begin = min(ntiles, split * p.tps);
@@ -341,21 +356,28 @@ void fwd_kernel(const FwdParams p) {
   for (int ks = 0; ks < KS; ++ks)
     qreg[ks] = buf_load16(rq, qoff + (uint32_t)((16 * ks + 8 * g) * 2)) ^ p.qneg;
 
-  // Tile t -> LDS stage: block q of K (and of V) is rows [q*RPB, +RPB);
-  // lane l fills physical chunk l % CPR of row q*RPB + l / CPR.
+  // Step t -> LDS stage: its key tiles (t, or KS2: 2t and 2t + 1 in slots
+  // 0 and 1); block q of K (and of V) is rows [q*RPB, +RPB); lane l fills
+  // physical chunk l % CPR of row q*RPB + l / CPR.
   auto issue_tile = [&](int t, int stage) __attribute__((always_inline)) {
     if (!loader) return;
 #pragma unroll
-    for (int i = 0; i < QPW; ++i) {
-      const int q = wave + i * NL;
-      if (BLOCKS % NL == 0 || q < BLOCKS) {
-        const int row = q * RPB + lane / CPR;
-        const int ch = (lane % CPR) ^ swz<D>(row);
-        const int key = t * BN + row;
-        const uint32_t lb = kv_base + (uint32_t)((stage * 2 * TILE + q * 512) * 2);
-        dma16(wk, (uint32_t)((key * p.sk2 + ch * 8) * 2), __builtin_amdgcn_readfirstlane(lb));
-        dma16(wv, (uint32_t)((key * p.sv2 + ch * 8) * 2),
-              __builtin_amdgcn_readfirstlane(lb + TILE * 2));
+    for (int slot = 0; slot < NTS; ++slot) {
+      const int tile = NTS * t + slot;
+      if (KS2 && tile >= ntiles) break;
+#pragma unroll
+      for (int i = 0; i < QPW; ++i) {
+        const int q = wave + i * NL;
+        if (BLOCKS % NL == 0 || q < BLOCKS) {
+          const int row = q * RPB + lane / CPR;
+          const int ch = (lane % CPR) ^ swz<D>(row);
+          const int key = tile * BN + row;
+          const uint32_t lb =
+              kv_base + (uint32_t)(((stage * NTS + slot) * 2 * TILE + q * 512) * 2);
+          dma16(wk, (uint32_t)((key * p.sk2 + ch * 8) * 2), __builtin_amdgcn_readfirstlane(lb));
+          dma16(wv, (uint32_t)((key * p.sv2 + ch * 8) * 2),
+                __builtin_amdgcn_readfirstlane(lb + TILE * 2));
+        }
       }
     }
   };
@@ -402,7 +424,10 @@ void fwd_kernel(const FwdParams p) {
       RowGeom gz = gs;
       gz.pos0 = mpos0;
       const int wa = wtiles_of(mrow0 + 32 * wave), wb = wtiles_of(mrow0 + 32 * pwave);
-      zr.init(mrow0 + 32 * wave, wa * BN, mrow0 + 32 * pwave, wb * BN, p.N, lane, gz);
+      if constexpr (KS2)  // the storer's slice of the mirror block (no second rectangle)
+        zr.init(mrow0 + 32 * pwave, wb * BN, 1 << 29, p.N, p.N, lane, gz);
+      else
+        zr.init(mrow0 + 32 * wave, wa * BN, mrow0 + 32 * pwave, wb * BN, p.N, lane, gz);
     }
   }
   // Staged score tile: row r (32 rows), 16-byte chunk ch (8 per row) at
@@ -456,15 +481,17 @@ void fwd_kernel(const FwdParams p) {
       buf_store16_nt(u32x4{0u, 0u, 0u, 0u}, rz, vb + 128u * (uint32_t)i, zr.koff);
     zr.advance();
   };
-  // Score tiles t of the partner (staged by wave pwave in iteration t) and of
-  // the storer itself (staged in iteration t, single buffer).
+  // Score tiles of step t of the partner (staged by wave pwave in step t)
+  // and of the storer itself (staged in step t, single buffer): key tile t
+  // of both, or (KS2, same rows) tiles 2t and 2t + 1.
   auto staged_pair = [&](int t, u32x4 (&w)[8], uint32_t (&o)[8]) __attribute__((always_inline)) {
     u32x4 wp[4], wo[4];
     uint32_t op[4], oo[4];
+    const int tp = NTS * t, to = NTS * t + (NTS - 1);
     read_staged(((t & 1) * NH + pwave) * TSZ, wp);
     read_staged((NW + pwave) * TSZ, wo);
-    staged_offsets(row0 + 32 * pwave, t * BN, t >= 0 && t < pwtiles, op);
-    staged_offsets(row0 + 32 * wave, t * BN, t >= 0 && t < wtiles, oo);
+    staged_offsets(row0 + 32 * pwave, tp * BN, t >= 0 && tp < pwtiles, op);
+    staged_offsets(row0 + 32 * slice, to * BN, t >= 0 && to < wtiles, oo);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       w[i] = wp[i];
@@ -639,13 +666,14 @@ void fwd_kernel(const FwdParams p) {
     auto step = [&](int it, auto stage_tag, auto mask_tag) __attribute__((always_inline)) {
       constexpr int stage = decltype(stage_tag)::value;
       constexpr bool MK = decltype(mask_tag)::value;
-      const bool masked = MK && it >= tfull;
+      const int tw = NTS * it + kpar;  // this wave's key tile
+      const bool masked = MK && tw >= tfull;
       if (it + 1 < t_end) issue_tile(it + 1, stage ^ 1);
-      const uint16_t* kt = kv[stage][0];
-      const uint16_t* vt = kv[stage][1];
-      const int k0 = it * BN;
+      const uint16_t* kt = kv[stage][kpar][0];
+      const uint16_t* vt = kv[stage][kpar][1];
+      const int k0 = tw * BN;
 
-      if (it < wtiles) {
+      if (tw < wtiles) {
         f32x16 s[2];
         if constexpr (ST) {
           // S = K Q^T with the partner's and its own tile it-1 stored in between.
@@ -836,7 +864,9 @@ void fwd_kernel(const FwdParams p) {
     // barrier each.
     using S0 = std::integral_constant<int, 0>;
     using S1 = std::integral_constant<int, 1>;
-    const int full_end = max(t_begin, min(tfull, t_end));
+    // (KS2: step it is full for this wave if its tile 2 it + kpar is.)
+    const int full_steps = KS2 ? max(0, tfull - kpar + 1) / 2 : tfull;
+    const int full_end = max(t_begin, min(full_steps, t_end));
     int it = t_begin;
     for (; it + 1 < full_end; it += 2) {
       step(it, S0{}, std::false_type{});
@@ -859,7 +889,7 @@ void fwd_kernel(const FwdParams p) {
     if (storer) {
       u32x4 w[8];
       uint32_t o[8];
-      staged_pair(ntiles - 1, w, o);
+      staged_pair(t_end - 1, w, o);
 #pragma unroll
       for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
       while (zr.pending()) zero_batch();
@@ -878,6 +908,34 @@ void fwd_kernel(const FwdParams p) {
     }
   }
 
+  if constexpr (KS2) {
+    // The storer's partial O, offset and weight sum meet its loader's in LDS
+    // (the K/V tiles' space, free after the loop); lane l of both holds the
+    // same row and head dims.
+    float* mb = reinterpret_cast<float*>(&kv[0][0][0][0]) + slice * (DB * 16 + 2) * 64;
+    lds_barrier();
+    if (!loader) {
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mb[(db * 16 + r) * 64 + lane] = oacc[db][r];
+      mb[DB * 16 * 64 + lane] = m_ref;
+      mb[(DB * 16 + 1) * 64 + lane] = l_i;
+    }
+    lds_barrier();
+    if (!loader) return;
+    const float mo = mb[DB * 16 * 64 + lane], lo = mb[(DB * 16 + 1) * 64 + lane];
+    const float mn = fmaxf(m_ref, mo);
+    const float a0 = m_ref == neg_inf() ? 0.f : exp2f_fast((m_ref - mn) * p.qk_scale);
+    const float a1 = mo == neg_inf() ? 0.f : exp2f_fast((mo - mn) * p.qk_scale);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        oacc[db][r] = oacc[db][r] * a0 + mb[(db * 16 + r) * 64 + lane] * a1;
+    l_i = l_i * a0 + lo * a1;
+    m_ref = mn;
+  }
   // Epilogue: O = acc / l, base-2 LSE, row sums.
   const float l_tot = xor32_add(l_i);
   if constexpr (kCanSplit) {
@@ -994,12 +1052,12 @@ __global__ __launch_bounds__(256) void fwd_combine_kernel(const FwdParams p) {
   }
 }
 
-template <class E, int D, int MODE, int NW, bool DROP, bool PACK>
+template <class E, int D, int MODE, int NW, bool DROP, bool PACK, bool KS2 = false>
 hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   constexpr bool kCanSplit = MODE == kFwdPlain || MODE == kFwdPlainKeepBits || MODE == kFwdRowSum;
   const int64_t nsplit = kCanSplit ? p.nsplit : 1;
   const dim3 grid((unsigned)((int64_t)p.nrb * (p.B * p.H / p.pack) * nsplit)), block(NW * 64);
-  hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW, DROP, PACK>), grid, block, 0, stream, p);
+  hipLaunchKernelGGL((fwd_kernel<E, D, MODE, NW, DROP, PACK, KS2>), grid, block, 0, stream, p);
   if constexpr (kCanSplit) {
     if (p.nsplit > 1 && p.M > 0) {
       const int64_t nblk = (p.M + 2048 / D - 1) / (2048 / D);
@@ -1011,21 +1069,21 @@ hipError_t launch_fwd_t(const FwdParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int MODE, int NW, bool DROP = false, bool PACK = false>
+template <int MODE, int NW, bool DROP = false, bool PACK = false, bool KS2 = false>
 hipError_t launch_fwd_mode(const FwdParams& p, int dtype, int d, hipStream_t s) {
   if (dtype == 0) {
     switch (d) {
-      case 16: return launch_fwd_t<F16, 16, MODE, NW, DROP, PACK>(p, s);
-      case 32: return launch_fwd_t<F16, 32, MODE, NW, DROP, PACK>(p, s);
-      case 64: return launch_fwd_t<F16, 64, MODE, NW, DROP, PACK>(p, s);
-      case 128: return launch_fwd_t<F16, 128, MODE, NW, DROP, PACK>(p, s);
+      case 16: return launch_fwd_t<F16, 16, MODE, NW, DROP, PACK, KS2>(p, s);
+      case 32: return launch_fwd_t<F16, 32, MODE, NW, DROP, PACK, KS2>(p, s);
+      case 64: return launch_fwd_t<F16, 64, MODE, NW, DROP, PACK, KS2>(p, s);
+      case 128: return launch_fwd_t<F16, 128, MODE, NW, DROP, PACK, KS2>(p, s);
     }
   } else {
     switch (d) {
-      case 16: return launch_fwd_t<BF16, 16, MODE, NW, DROP, PACK>(p, s);
-      case 32: return launch_fwd_t<BF16, 32, MODE, NW, DROP, PACK>(p, s);
-      case 64: return launch_fwd_t<BF16, 64, MODE, NW, DROP, PACK>(p, s);
-      case 128: return launch_fwd_t<BF16, 128, MODE, NW, DROP, PACK>(p, s);
+      case 16: return launch_fwd_t<BF16, 16, MODE, NW, DROP, PACK, KS2>(p, s);
+      case 32: return launch_fwd_t<BF16, 32, MODE, NW, DROP, PACK, KS2>(p, s);
+      case 64: return launch_fwd_t<BF16, 64, MODE, NW, DROP, PACK, KS2>(p, s);
+      case 128: return launch_fwd_t<BF16, 128, MODE, NW, DROP, PACK, KS2>(p, s);
     }
   }
   return hipErrorInvalidValue;

@@ -14,11 +14,12 @@ hipError_t launch_fwd_scores_packed(const FwdParams& p, int dtype, int d, hipStr
 // GQA-packed launches (p.pack > 1) take their own instances; the host never
 // packs a launch with dropout.
 hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, hipStream_t s) {
-  // Only the unpacked score writer without dropout has a 128-row instance;
-  // every other launch is built for 256-row blocks.
-  if (p.bm != kFwdRows && !(p.bm == kFwdRows / 2 && mode == kFwdScores && p.pack == 1 &&
-                            !p.dropout))
-    return hipErrorInvalidValue;
+  // Only the unpacked score writer without dropout has 128-row and (key
+  // split, 16-byte score rows) 64-row instances; every other launch is built
+  // for 256-row blocks.
+  const bool small_writer = mode == kFwdScores && p.pack == 1 && !p.dropout &&
+                            (p.bm == kFwdRows / 2 || (p.bm == kFwdRows / 4 && p.vec_scores));
+  if (p.bm != kFwdRows && !small_writer) return hipErrorInvalidValue;
   if (p.pack > 1) {
     if (p.dropout && mode != kFwdRegion) return hipErrorInvalidValue;
     return mode == kFwdScores ? launch_fwd_scores_packed(p, dtype, d, s)

@@ -305,3 +305,31 @@ def test_gqa_equals_mha_on_repeated_kv(ep, gpu):
         assert_sum_close(x1, x2.view(B, Hk, Hq // Hk, -1).sum(2), ep)
     else:
         assert_sum_close(x1, x2, ep)
+
+
+# Causal score writes whose 128-row blocks all fit in one round of workgroups
+# with long rows (N >= 2048) take the key-split writer: 64-row blocks whose
+# even and odd key tiles go to two wave pairs, merged at the end.  Ragged M
+# and N (N % 64 != 0, a last step with one tile), M < N, M > N (rows that see
+# no key), every head dim, both dtypes, a group of 3 query heads per KV head
+# (the writer packs only 2, 4 or 8, so these stay unpacked) and a large input
+# scale (maxima that differ between the two halves of a row's keys).
+KEY_SPLIT_SHAPES = [
+    (1, 2, 2, 2048, 2048, 128),
+    (1, 2, 2, 2112, 2112, 64),
+    (1, 1, 1, 2000, 2056, 32),
+    (1, 2, 2, 100, 2048, 16),
+    (1, 1, 1, 2300, 2048, 128),
+    (2, 3, 1, 513, 2200, 64),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("shape", KEY_SPLIT_SHAPES, ids=_label)
+def test_scores_key_split_writer(shape, dtype, gpu):
+    _run("attention_with_scores", shape, dtype, True, gpu, seed=11)
+
+
+def test_scores_key_split_writer_large_inputs(gpu):
+    _run("attention_with_scores", (1, 2, 2, 2048, 2048, 128), torch.float16, True, gpu, seed=12,
+         scale=6.0)
