@@ -158,3 +158,41 @@ def test_metric_shape_softmax_col_sum(gpu):
                                       want=("out", "col_softmax"))
         assert_out_close(o[:, h:h + 1], ref["out"])
         assert_sum_close(col[:, h:h + 1], ref["col_softmax"], f"col_softmax head {h}")
+
+
+# The softmax column passes fold a KV head's G query heads inside the kernel:
+# one workgroup per key-block pair walking all G heads (nsplit 1), or the
+# heads dealt to nsplit workgroups (heads s, s + nsplit, ...) whose column
+# sums the last to finish adds through a device-scope ticket.  Shapes chosen
+# so the plan (tests/test_host.py::_col_plan, the host rule restated) takes
+# each regime, including uneven head sets (G = 3 over 2 splits, G = 7 over 4).
+HEAD_SPLIT_CASES = [
+    # (B, Hq, Hk, S, D, expected nsplit)
+    (4, 96, 32, 256, 64, 2),
+    (2, 224, 32, 256, 32, 4),
+    (8, 64, 32, 256, 64, 1),
+    (1, 8, 2, 1024, 128, 4),
+]
+
+
+@pytest.mark.parametrize("case", HEAD_SPLIT_CASES, ids=lambda c: "B{}H{}K{}S{}D{}ns{}".format(*c))
+def test_softmax_sums_head_split_plans(case, gpu):
+    from tests.test_host import _col_plan
+    B, Hq, Hk, S, D, ns = case
+    assert _col_plan(B, Hq, Hk, S, False)[0] == ns
+    print(f"[case] head split B{B} H{Hq}/{Hk} S{S} D{D} nsplit {ns}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, S, S, D, dtype=torch.float16, seed=21)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    _, col = fas.attention_with_softmax_col_sum(qd, kd, vd, causal=True)
+    split = S // 3
+    _, xsm = fas.attention_cross_token_softmax_sum(qd, kd, vd, split, causal=True)
+    _, xsb = fas.attention_cross_token_softmax_sum_buffered(qd, kd, vd, split, causal=True)
+    torch.cuda.synchronize()
+    ref = naive.reference_forward(q, k, v, causal=True, want=("col_softmax",))
+    assert_sum_close(col, ref["col_softmax"], "col_softmax")
+    xref = naive.reference_forward(q, k, v, causal=True, split=split, want=("cross_softmax",))
+    assert_sum_close(xsm, xref["cross_softmax"], "cross_softmax")
+    assert_sum_close(xsb, xref["cross_softmax"], "cross_softmax buffered")
+    # Repeat calls: the same bits (the fold adds partials in split order).
+    _, col2 = fas.attention_with_softmax_col_sum(qd, kd, vd, causal=True)
+    assert torch.equal(col, col2)
