@@ -361,6 +361,11 @@ void fwd_kernel(const FwdParams p) {
   // physical chunk l % CPR of row q*RPB + l / CPR.
   auto issue_tile = [&](int t, int stage) __attribute__((always_inline)) {
     if (!loader) return;
+    // The LDS destinations are formed from the base in each step (an opaque
+    // copy per tile), not hoisted out of the loop as 2*QPW scalars per stage
+    // that would be spilled.
+    uint32_t kvb = kv_base;
+    asm("" : "+s"(kvb) : "s"(t));
 #pragma unroll
     for (int slot = 0; slot < NTS; ++slot) {
       const int tile = NTS * t + slot;
@@ -373,7 +378,7 @@ void fwd_kernel(const FwdParams p) {
           const int ch = (lane % CPR) ^ swz<D>(row);
           const int key = tile * BN + row;
           const uint32_t lb =
-              kv_base + (uint32_t)(((stage * NTS + slot) * 2 * TILE + q * 512) * 2);
+              kvb + (uint32_t)(((stage * NTS + slot) * 2 * TILE + q * 512) * 2);
           dma16(wk, (uint32_t)((key * p.sk2 + ch * 8) * 2), __builtin_amdgcn_readfirstlane(lb));
           dma16(wv, (uint32_t)((key * p.sv2 + ch * 8) * 2),
                 __builtin_amdgcn_readfirstlane(lb + TILE * 2));
@@ -390,7 +395,7 @@ void fwd_kernel(const FwdParams p) {
   const int pwave = wave - NH;  // the loader wave a storer serves
   const int pwtiles = kSplit ? wtiles_of(row0 + 32 * pwave) : 0;
   // Lane (row l/8, chunk l%8) of an 8-row x 128-byte store.
-  const int lane_key = 8 * (lane & 7);
+  int lane_key = 8 * (lane & 7);
   __amdgpu_buffer_rsrc_t rs = make_rsrc(p.scores, 0);
   __amdgpu_buffer_rsrc_t rz = rs;
   ZeroRuns<PACK> zr;
@@ -885,8 +890,16 @@ void fwd_kernel(const FwdParams p) {
   } else {
     main_loop(std::false_type{});
   }
+  // Lane-derived values used after the key loop are formed again from an
+  // opaque copy of the lane id instead of being carried through the loop
+  // (where the score writer has no register left for them).
+  int lane_e = lane;
+  asm volatile("" : "+v"(lane_e));
   if constexpr (MODE == kFwdScores) {
     if (storer) {
+      lane_key = 8 * (lane_e & 7);
+      lane_off = gs.lane_off(lane_e);
+      zr.lane_off = lane_off;
       u32x4 w[8];
       uint32_t o[8];
       staged_pair(t_end - 1, w, o);
@@ -968,6 +981,7 @@ void fwd_kernel(const FwdParams p) {
       return;
     }
   }
+  const int g_e = lane_e >> 5;
   float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if constexpr (DROP) inv *= p.drop.scale;
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(p.o + b * p.so0 + h0 * p.so1, p.o_bytes);
@@ -975,7 +989,7 @@ void fwd_kernel(const FwdParams p) {
   for (int db = 0; db < DB; ++db)
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const int d0 = 32 * db + 16 * hf + 8 * g;
+      const int d0 = 32 * db + 16 * hf + 8 * g_e;
       if (d0 < D) {
         const f32x16& o = oacc[db];
         const int r0 = 8 * hf;
