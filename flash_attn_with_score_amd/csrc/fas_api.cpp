@@ -959,7 +959,12 @@ static int attention_with_scores_impl(const fas_attn_args* a, void* scores, cons
         (int64_t)pr.B * pr.H * ((pr.M + bm - 1) / bm) <= cus)
       bm = fas::kFwdRows / 4;
   }
+  // 128-row blocks that all run in one round: the 8-wave key-split writer
+  // (two waves per SIMD on each block's even and odd key tiles).
+  const int key_split2 = bm == fas::kFwdRows / 2 && vec_scores &&
+                         (int64_t)pr.B * pr.H * ((pr.M + bm - 1) / bm) <= cus;
   fas::FwdParams p = fwd_params(a, pw, false, bm);
+  p.key_split2 = key_split2;
   rescale_dropout(p, a);
   p.scores = static_cast<uint16_t*>(scores);
   p.ss0 = st[0];

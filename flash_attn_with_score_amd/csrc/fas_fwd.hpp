@@ -197,14 +197,14 @@ struct ZeroRuns {
   }
 };
 
-// Scheduling hint for a storer's MFMA phase: alternate two MFMAs and one
+// Scheduling hint for a storer's MFMA phase: alternate M MFMAs and one
 // global store, so each store finds room in the CU's store queue and the
 // wave never stalls on a burst.
-template <int N>
+template <int N, int M = 2>
 __device__ __forceinline__ void interleave_mfma_stores() {
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x008, M, 0);  // MFMA
     __builtin_amdgcn_sched_group_barrier(0x040, 1, 0);  // VMEM write
   }
 }
@@ -225,25 +225,44 @@ __device__ __forceinline__ void sched_score_tile() {
   if (NST > KS) __builtin_amdgcn_sched_group_barrier(0x040, NST > KS ? NST - KS : 1, 0);
 }
 
+// LDS of the region mode's row-major staging (kFwdRegion only: other
+// instances never instantiate these, so their LDS holds none of it).
+template <int NW>
+__device__ __forceinline__ f32x4* region_stage() {
+  __shared__ __attribute__((aligned(16))) f32x4 a[NW * 512];
+  return a;
+}
+template <int BM>
+__device__ __forceinline__ int64_t* region_rows() {
+  __shared__ int64_t a[BM];
+  return a;
+}
+
 // PACK: GQA packing (p.pack query heads per workgroup, per-lane heads and
 // positions); without it the workgroup's rows are one head's and every
 // per-lane head offset folds away at compile time.
 // Two waves per SIMD, except for the 4-wave score writer, whose LDS (one
 // workgroup per CU) allows one.
-// KS2 (4-wave score writer only): 64-row blocks whose key range is split
-// between the wave pairs: loader wave i takes the even key tiles and storer
-// wave 2 + i the odd ones of the same 32 rows, so a step stages two key
-// tiles; at the end each storer hands its partial O, offset and weight sum
-// to its loader through LDS.  For problems whose 128-row blocks all run in
-// one round, where the longest causal row block alone set the kernel time:
-// 64-row blocks run in two rounds whose longest-first pairs (rb, 15 - rb)
-// all take the same number of steps.
+// KS2 (unpacked score writer): row blocks of 32 * NW / 2 rows whose key
+// range is split between the wave pairs: loader wave i takes the even key
+// tiles and storer wave NW/2 + i the odd ones of the same 32 rows, so a step
+// stages two key tiles; at the end each storer hands its partial O, offset
+// and weight sum to its loader through LDS.  For problems whose 128-row
+// blocks all run in one round, where the longest causal row block alone set
+// the kernel time:
+//  * 4 waves, 64-row blocks: two rounds whose longest-first pairs (rb,
+//    15 - rb) all take the same number of steps (one wave per SIMD);
+//  * 8 waves, 128-row blocks: one round at two waves per SIMD, half the steps
+//    of the 4-wave 128-row writer per row block.  Its K/V stages fill 128 KiB
+//    of LDS, so the loaders' score tiles are single-buffered: a second
+//    barrier in each step (after the tiles are staged) hands them to the
+//    storers, which store both tiles of the step during O += P V.
 template <class E, int D, int MODE, int NW, bool DROP, bool PACK, bool KS2 = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 4 ? 1 : 2, 2)))
 void fwd_kernel(const FwdParams p) {
   static_assert(MODE != kFwdScores || NW == 8 || NW == 4, "the score writer uses 4 or 8 waves");
-  static_assert(!KS2 || (MODE == kFwdScores && NW == 4 && !DROP && !PACK),
-                "the key-split writer is the unpacked 4-wave score writer");
+  static_assert(!KS2 || (MODE == kFwdScores && !DROP && !PACK),
+                "the key-split writer is the unpacked score writer");
   constexpr int NH = NW / 2;  // score writer: loader waves [0, NH), storer waves [NH, NW)
   const int pack = PACK ? p.pack : 1;
   constexpr int KS = D / 16;               // MFMA k-steps over the head dim
@@ -260,21 +279,36 @@ void fwd_kernel(const FwdParams p) {
   constexpr int QPW = (BLOCKS + NL - 1) / NL;
   // Score tiles leave through LDS (4 KiB per 32-row wave tile), so that
   // every global store instruction writes 8 full 128-byte row segments:
-  // 2 stages x NH loader tiles, then one tile per storer.
+  // 2 stages x NH loader tiles, then one tile per storer (kMid: one stage of
+  // loader tiles, handed over within the step).
+  constexpr bool kMid = KS2 && NW == 8;
   constexpr int TSZ = 256;  // 16-byte units per wave tile
-  constexpr int SG = kSplit ? 3 * NH * TSZ : 1;
+  constexpr int SG = kSplit ? (kMid ? 2 : 3) * NH * TSZ : 1;
+  constexpr int kLoaderStg = kMid ? 1 : 2;  // stages of loader tiles
+  constexpr int kOwnStg = kLoaderStg * NH;  // first storer tile
   // Zero-store slots per key tile and storer (issued during O += P V).
   constexpr int kZero = 8;  // zero stores per key tile: one ZeroRuns batch
 
-  __shared__ __attribute__((aligned(16))) uint16_t kv[2][NTS][2][TILE];
+  // K/V stages; after the key loop (KS2) the storers' partial O, offsets and
+  // weight sums pass through the same LDS, which is sized for the larger.
+  union KvLds {
+    uint16_t t[2][NTS][2][TILE];
+    float merge[KS2 ? NH * (DB * 16 + 2) * 64 : 1];
+  };
+  __shared__ __attribute__((aligned(16))) KvLds kv_lds;
+  auto& kv = kv_lds.t;
   __shared__ __attribute__((aligned(16))) u32x4 stg[SG];
   // Region tiles (kFwdRegion) leave through LDS too: a wave's 32 x 64 fp32
   // tile (8 KiB, 16-byte chunks XOR-swizzled by row) is read back row-major,
   // so each store writes four whole 256-byte row segments; rofs holds each
   // virtual row's element offset in the region (-1 outside it).
   constexpr bool kRegion = MODE == kFwdRegion;
-  __shared__ __attribute__((aligned(16))) f32x4 rstg[kRegion ? NW * 512 : 1];
-  __shared__ int64_t rofs[kRegion ? BM : 1];
+  f32x4* rstg = nullptr;
+  int64_t* rofs = nullptr;
+  if constexpr (kRegion) {
+    rstg = region_stage<NW>();
+    rofs = region_rows<BM>();
+  }
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
@@ -359,11 +393,17 @@ void fwd_kernel(const FwdParams p) {
   // Step t -> LDS stage: its key tiles (t, or KS2: 2t and 2t + 1 in slots
   // 0 and 1); block q of K (and of V) is rows [q*RPB, +RPB); lane l fills
   // physical chunk l % CPR of row q*RPB + l / CPR.
+  // The global offset of a lane's 16 bytes, (key * stride + 8 ch) * 2, is a
+  // per-lane part (its row within the block and its chunk; the swizzle of
+  // row q*RPB + l/CPR repeats with period PQ in q) plus the uniform
+  // (tile * BN + q * RPB) * stride * 2, and the LDS destination is the
+  // stage base plus a constant.  Each part passes through an opaque copy per
+  // step: hoisted out of the loop, the 2*QPW*NTS offsets and destinations
+  // per stage were kept in registers the loop lacks (spilled).
+  constexpr int PQ = D == 128 ? 4 : (D == 64 ? 2 : 1);
+  const uint32_t sk2 = (uint32_t)p.sk2, sv2 = (uint32_t)p.sv2;
   auto issue_tile = [&](int t, int stage) __attribute__((always_inline)) {
     if (!loader) return;
-    // The LDS destinations are formed from the base in each step (an opaque
-    // copy per tile), not hoisted out of the loop as 2*QPW scalars per stage
-    // that would be spilled.
     uint32_t kvb = kv_base;
     asm("" : "+s"(kvb) : "s"(t));
 #pragma unroll
@@ -374,19 +414,21 @@ void fwd_kernel(const FwdParams p) {
       for (int i = 0; i < QPW; ++i) {
         const int q = wave + i * NL;
         if (BLOCKS % NL == 0 || q < BLOCKS) {
-          const int row = q * RPB + lane / CPR;
-          const int ch = (lane % CPR) ^ swz<D>(row);
-          const int key = tile * BN + row;
+          const int rl = lane / CPR;
+          const int ch = (lane % CPR) ^ swz<D>((q % PQ) * RPB + rl);
+          uint32_t lk = (uint32_t)(rl * sk2 + ch * 8) * 2u;
+          uint32_t lv = (uint32_t)(rl * sv2 + ch * 8) * 2u;
+          asm("" : "+v"(lk), "+v"(lv) : "s"(t));
+          uint32_t kr = (uint32_t)(tile * BN + q * RPB);
+          asm("" : "+s"(kr));
           const uint32_t lb =
               kvb + (uint32_t)(((stage * NTS + slot) * 2 * TILE + q * 512) * 2);
-          dma16(wk, (uint32_t)((key * p.sk2 + ch * 8) * 2), __builtin_amdgcn_readfirstlane(lb));
-          dma16(wv, (uint32_t)((key * p.sv2 + ch * 8) * 2),
-                __builtin_amdgcn_readfirstlane(lb + TILE * 2));
+          dma16(wk, lk + kr * sk2 * 2u, __builtin_amdgcn_readfirstlane(lb));
+          dma16(wv, lv + kr * sv2 * 2u, __builtin_amdgcn_readfirstlane(lb + TILE * 2));
         }
       }
     }
   };
-
   // ---- score writer state (kFwdScores) ----
   // Storers exist only for 16-byte aligned score rows; otherwise every wave
   // writes its own scores element-wise.
@@ -493,8 +535,8 @@ void fwd_kernel(const FwdParams p) {
     u32x4 wp[4], wo[4];
     uint32_t op[4], oo[4];
     const int tp = NTS * t, to = NTS * t + (NTS - 1);
-    read_staged(((t & 1) * NH + pwave) * TSZ, wp);
-    read_staged((NW + pwave) * TSZ, wo);
+    read_staged(((kMid ? 0 : (t & 1)) * NH + pwave) * TSZ, wp);
+    read_staged((kOwnStg + pwave) * TSZ, wo);
     staged_offsets(row0 + 32 * pwave, tp * BN, t >= 0 && tp < pwtiles, op);
     staged_offsets(row0 + 32 * slice, to * BN, t >= 0 && to < wtiles, oo);
 #pragma unroll
@@ -515,12 +557,31 @@ void fwd_kernel(const FwdParams p) {
   // Every K operand fetch is written before the MFMAs; the caller pins the
   // schedule (sched_score_tile) so each fetch runs PD k-steps ahead of the
   // MFMAs that consume it and no MFMA waits on a fresh LDS read.
-  auto score_tile = [&](const uint16_t* kt, f32x16 (&s)[2]) __attribute__((always_inline)) {
+  // XA (tile index tw): the fetch addresses are formed in the call as
+  // kaddr ^ (ks << 5) from an opaque per-tile copy of the lane's byte offset
+  // kaddr of k-step 0 (row perm_row(c), logical chunk g: chunk 2ks + g is
+  // physical 2ks ^ (g ^ swz(row)), and row * 2D has no bit below 2D), instead
+  // of KS loop-invariant addresses held in registers through the key loop.
+  const uint32_t kaddr = (uint32_t)(2 * tile_off<D>(perm_row(c), g));
+  auto score_tile = [&](const uint16_t* kt, f32x16 (&s)[2], int tw, auto xa)
+                        __attribute__((always_inline)) {
     u32x4 a0[KS], a1[KS];
+    if constexpr (decltype(xa)::value) {
+      uint32_t ka = kaddr;
+      asm("" : "+v"(ka) : "s"(tw));
+      const char* kb = reinterpret_cast<const char*>(kt);
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      a0[ks] = lds_row_chunk<D>(kt, perm_row(c), ks, g);
-      a1[ks] = lds_row_chunk<D>(kt, 32 + perm_row(c), ks, g);
+      for (int ks = 0; ks < KS; ++ks) {
+        const uint32_t off = ka ^ (uint32_t)(ks << 5);
+        a0[ks] = *reinterpret_cast<const u32x4*>(kb + off);
+        a1[ks] = *reinterpret_cast<const u32x4*>(kb + off + 64 * D);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        a0[ks] = lds_row_chunk<D>(kt, perm_row(c), ks, g);
+        a1[ks] = lds_row_chunk<D>(kt, 32 + perm_row(c), ks, g);
+      }
     }
     s[0] = f32x16{};
     s[1] = f32x16{};
@@ -636,6 +697,38 @@ void fwd_kernel(const FwdParams p) {
           0, 0);
     }
   };
+  // Online softmax, base 2, on raw scores.  Offset update: the tile maximum
+  // (combined over the two half-waves of a row) raises a row's offset m_ref
+  // when it exceeds it by more than 2^8 in the base-2 exponent, rescaling
+  // that row's O and l.
+  auto update_offset_of = [&](const f32x16 (&s)[2]) __attribute__((always_inline)) {
+    float mx = neg_inf();
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = xor32_max(mx);
+    const bool grow = mx > m_ref && (m_ref == neg_inf() || (mx - m_ref) * p.qk_scale > 8.f);
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? mx : m_ref;
+      const float alpha = m_ref == neg_inf() ? 0.f : exp2f_fast((m_ref - m_new) * p.qk_scale);
+      l_i *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+      m_ref = m_new;
+    }
+  };
+  // Causal / key-range mask of a tile starting at key k0: masked -> -inf.
+  auto apply_mask = [&](f32x16 (&s)[2], int k0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int key = k0 + 32 * kb + acc_row(r, g);
+        const bool ok = key < p.N && (!p.causal || p.causal_off + qpos >= key);
+        if (!ok) s[kb][r] = neg_inf();
+      }
+  };
   auto pv_mma = [&](const u32x4 (&pb)[4], const uint16_t* vt) __attribute__((always_inline)) {
 #pragma unroll
     for (int db = 0; db < DB; ++db)
@@ -663,6 +756,7 @@ void fwd_kernel(const FwdParams p) {
   // merges with the other inside the loop.
   auto main_loop = [&](auto role) __attribute__((always_inline)) {
     constexpr bool ST = decltype(role)::value;
+
     // One key tile; the LDS stage is a compile-time constant, so the
     // per-lane operand addresses are loop-invariant and the stage offset
     // folds into the LDS instructions' immediate offsets. Only the copy
@@ -671,14 +765,59 @@ void fwd_kernel(const FwdParams p) {
     auto step = [&](int it, auto stage_tag, auto mask_tag) __attribute__((always_inline)) {
       constexpr int stage = decltype(stage_tag)::value;
       constexpr bool MK = decltype(mask_tag)::value;
-      const int tw = NTS * it + kpar;  // this wave's key tile
+      // KS2: the storers (the ST copy; KS2 launches always have storers)
+      // take the odd tiles.  A compile-time slot keeps the LDS operand
+      // addresses of the two roles apart; with the slot a runtime value
+      // every address carried it and the storer's loop spilled.
+      constexpr int kp = KS2 && ST ? 1 : 0;
+      const int tw = NTS * it + kp;  // this wave's key tile
       const bool masked = MK && tw >= tfull;
       if (it + 1 < t_end) issue_tile(it + 1, stage ^ 1);
-      const uint16_t* kt = kv[stage][kpar][0];
-      const uint16_t* vt = kv[stage][kpar][1];
+      const uint16_t* kt = kv[stage][kp][0];
+      const uint16_t* vt = kv[stage][kp][1];
       const int k0 = tw * BN;
 
-      if (tw < wtiles) {
+      if constexpr (kMid) {
+        // As below (the storer reads back the tiles of the step before and
+        // stores them between its S MFMAs), but a barrier after S lets every
+        // storer finish that read-back before any wave stages this step's
+        // tile into the single buffer.
+        const bool act = tw < wtiles;
+        f32x16 s[2];
+        if constexpr (ST) {
+          u32x4 w[8];
+          uint32_t o[8];
+          staged_pair(it - 1, w, o);
+          if (act) {
+            __builtin_amdgcn_sched_barrier(0);
+            score_tile(kt, s, tw, std::true_type{});
+#pragma unroll
+            for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
+            sched_score_tile<KS, 8>();
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
+          }
+        } else if (act) {
+          score_tile(kt, s, tw, std::true_type{});
+          sched_score_tile<KS, 0>();
+        }
+        lds_barrier();
+        if (act) {
+          if (masked) apply_mask(s, k0);
+          stage_tile((loader ? wave : kOwnStg + pwave) * TSZ, s, masked);
+          update_offset_of(s);
+          u32x4 pb[4];
+          l_i += make_p(s, pb);
+          pv_mma(pb, vt);
+          if constexpr (ST) {
+            zero_batch();
+            interleave_mfma_stores<kZero>();
+          }
+        } else if constexpr (ST) {
+          zero_batch();
+        }
+      } else if (tw < wtiles) {
         f32x16 s[2];
         if constexpr (ST) {
           // S = K Q^T with the partner's and its own tile it-1 stored in between.
@@ -686,24 +825,15 @@ void fwd_kernel(const FwdParams p) {
           uint32_t o[8];
           staged_pair(it - 1, w, o);
           __builtin_amdgcn_sched_barrier(0);
-          score_tile(kt, s);
+          score_tile(kt, s, 0, std::false_type{});
 #pragma unroll
           for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
           sched_score_tile<KS, 8>();
         } else {
-          score_tile(kt, s);
+          score_tile(kt, s, 0, std::false_type{});
           sched_score_tile<KS, 0>();
         }
-        if (masked) {
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int key = k0 + 32 * kb + acc_row(r, g);
-              const bool ok = key < p.N && (!p.causal || p.causal_off + qpos >= key);
-              if (!ok) s[kb][r] = neg_inf();
-            }
-        }
+        if (masked) apply_mask(s, k0);
 
         if constexpr (MODE == kFwdScores) {
           if (vec) {
@@ -796,29 +926,7 @@ void fwd_kernel(const FwdParams p) {
           }
         }
 
-        // Online softmax, base 2, on raw scores.  Offset update: the tile
-        // maximum (combined over the two half-waves of a row) raises a row's
-        // offset m_ref when it exceeds it by more than 2^8 in the base-2
-        // exponent, rescaling that row's O and l.
-        auto update_offset = [&]() __attribute__((always_inline)) {
-          float mx = neg_inf();
-#pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-          mx = xor32_max(mx);
-          const bool grow =
-              mx > m_ref && (m_ref == neg_inf() || (mx - m_ref) * p.qk_scale > 8.f);
-          if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-            const float m_new = grow ? mx : m_ref;
-            const float alpha =
-                m_ref == neg_inf() ? 0.f : exp2f_fast((m_ref - m_new) * p.qk_scale);
-            l_i *= alpha;
-#pragma unroll
-            for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
-            m_ref = m_new;
-          }
-        };
+        auto update_offset = [&]() __attribute__((always_inline)) { update_offset_of(s); };
         u32x4 pb[4];
         float lt;
         if constexpr (MODE == kFwdScores) {
@@ -925,7 +1033,7 @@ void fwd_kernel(const FwdParams p) {
     // The storer's partial O, offset and weight sum meet its loader's in LDS
     // (the K/V tiles' space, free after the loop); lane l of both holds the
     // same row and head dims.
-    float* mb = reinterpret_cast<float*>(&kv[0][0][0][0]) + slice * (DB * 16 + 2) * 64;
+    float* mb = kv_lds.merge + slice * (DB * 16 + 2) * 64;
     lds_barrier();
     if (!loader) {
 #pragma unroll

@@ -18,7 +18,9 @@ hipError_t launch_fwd(const FwdParams& p, int mode, int dtype, int d, hipStream_
   // split, 16-byte score rows) 64-row instances; every other launch is built
   // for 256-row blocks.
   const bool small_writer = mode == kFwdScores && p.pack == 1 && !p.dropout &&
-                            (p.bm == kFwdRows / 2 || (p.bm == kFwdRows / 4 && p.vec_scores));
+                            ((p.bm == kFwdRows / 2 && (!p.key_split2 || p.vec_scores)) ||
+                             (p.bm == kFwdRows / 4 && p.vec_scores));
+  if (p.key_split2 && !(small_writer && p.bm == kFwdRows / 2)) return hipErrorInvalidValue;
   if (p.bm != kFwdRows && !small_writer) return hipErrorInvalidValue;
   if (p.pack > 1) {
     if (p.dropout && mode != kFwdRegion) return hipErrorInvalidValue;

@@ -78,6 +78,8 @@ struct FwdParams {
   int zero_self;     // score writer: 1 = a workgroup writes its own row block's zeros
                      // (all workgroups run at once), 0 = its mirror row block's
   int vec_region;    // split % 4 == 0
+  int key_split2;    // score writer with 128-row blocks: 1 = the 8-wave key-split
+                     // instance (wave pairs take the even and odd key tiles)
   int dropout;       // 1: the dropout instances (modes other than kFwdRegion)
   DropParams drop;   // scale also applies in the key-split combine (1 without dropout)
   // kFwdPlainKeepBits: the keep decisions as bits, word
