@@ -784,9 +784,9 @@ void fwd_kernel(const FwdParams p) {
         // tile into the single buffer.
         const bool act = tw < wtiles;
         f32x16 s[2];
+        u32x4 w[8];
+        uint32_t o[8];
         if constexpr (ST) {
-          u32x4 w[8];
-          uint32_t o[8];
           staged_pair(it - 1, w, o);
           if (act) {
             __builtin_amdgcn_sched_barrier(0);
@@ -809,6 +809,11 @@ void fwd_kernel(const FwdParams p) {
           update_offset_of(s);
           u32x4 pb[4];
           l_i += make_p(s, pb);
+          if constexpr (ST) {
+            // Keep the stored tiles' registers until the weights are formed.
+#pragma unroll
+            for (int i = 0; i < 8; ++i) asm volatile("" ::"v"(w[i]));
+          }
           pv_mma(pb, vt);
           if constexpr (ST) {
             zero_batch();
@@ -819,18 +824,18 @@ void fwd_kernel(const FwdParams p) {
         }
       } else if (tw < wtiles) {
         f32x16 s[2];
+        u32x4 w[8];
         if constexpr (ST) {
           // S = K Q^T with the partner's and its own tile it-1 stored in between.
-          u32x4 w[8];
           uint32_t o[8];
           staged_pair(it - 1, w, o);
           __builtin_amdgcn_sched_barrier(0);
-          score_tile(kt, s, 0, std::false_type{});
+          score_tile(kt, s, tw, std::integral_constant<bool, kSplit>{});
 #pragma unroll
           for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
           sched_score_tile<KS, 8>();
         } else {
-          score_tile(kt, s, 0, std::false_type{});
+          score_tile(kt, s, tw, std::integral_constant<bool, kSplit>{});
           sched_score_tile<KS, 0>();
         }
         if (masked) apply_mask(s, k0);
@@ -951,6 +956,11 @@ void fwd_kernel(const FwdParams p) {
           }
         }
         l_i += lt;
+        if constexpr (ST) {
+          // Keep the stored tiles' registers until the weights are formed.
+#pragma unroll
+          for (int i = 0; i < 8; ++i) asm volatile("" ::"v"(w[i]));
+        }
         if constexpr (DROP) drop_p(pb, k0);
         if constexpr (ST) {
           // O += P V with zero slots in between.
