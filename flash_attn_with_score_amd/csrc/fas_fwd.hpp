@@ -754,8 +754,12 @@ void fwd_kernel(const FwdParams p) {
 
   // The key-tile loop, instantiated once per wave role so that neither copy
   // merges with the other inside the loop.
-  auto main_loop = [&](auto role) __attribute__((always_inline)) {
+  // NZ (storer copy for a workgroup with no zeros to write, e.g. every
+  // non-causal one): the step's score stores go between the O += P V MFMAs,
+  // where the zero batches would be, and the S MFMAs run without stores.
+  auto main_loop = [&](auto role, auto nz_tag) __attribute__((always_inline)) {
     constexpr bool ST = decltype(role)::value;
+    constexpr bool NZ = ST && decltype(nz_tag)::value;
 
     // One key tile; the LDS stage is a compile-time constant, so the
     // per-lane operand addresses are loop-invariant and the stage offset
@@ -825,15 +829,19 @@ void fwd_kernel(const FwdParams p) {
       } else if (tw < wtiles) {
         f32x16 s[2];
         u32x4 w[8];
+        uint32_t o[8];
         if constexpr (ST) {
           // S = K Q^T with the partner's and its own tile it-1 stored in between.
-          uint32_t o[8];
           staged_pair(it - 1, w, o);
           __builtin_amdgcn_sched_barrier(0);
           score_tile(kt, s, tw, std::integral_constant<bool, kSplit>{});
+          if constexpr (!NZ) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
-          sched_score_tile<KS, 8>();
+            for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
+            sched_score_tile<KS, 8>();
+          } else {
+            sched_score_tile<KS, 0>();
+          }
         } else {
           score_tile(kt, s, tw, std::integral_constant<bool, kSplit>{});
           sched_score_tile<KS, 0>();
@@ -963,9 +971,14 @@ void fwd_kernel(const FwdParams p) {
         }
         if constexpr (DROP) drop_p(pb, k0);
         if constexpr (ST) {
-          // O += P V with zero slots in between.
+          // O += P V with zero slots (NZ: the score stores) in between.
           pv_mma(pb, vt);
-          zero_batch();
+          if constexpr (NZ) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
+          } else {
+            zero_batch();
+          }
           interleave_mfma_stores<kZero>();
         } else {
           pv_mma(pb, vt);
@@ -1001,12 +1014,22 @@ void fwd_kernel(const FwdParams p) {
     }
   };
   if constexpr (kSplit) {
-    if (storer)
-      main_loop(std::true_type{});
-    else
-      main_loop(std::false_type{});
+    if (storer) {
+      // (Packed GQA writers keep one storer copy: their registers have no
+      // room for a second.)
+      if constexpr (kMid || PACK) {
+        main_loop(std::true_type{}, std::false_type{});
+      } else {
+        if (zr.pending())
+          main_loop(std::true_type{}, std::false_type{});
+        else
+          main_loop(std::true_type{}, std::true_type{});
+      }
+    } else {
+      main_loop(std::false_type{}, std::false_type{});
+    }
   } else {
-    main_loop(std::false_type{});
+    main_loop(std::false_type{}, std::false_type{});
   }
   // Lane-derived values used after the key loop are formed again from an
   // opaque copy of the lane id instead of being carried through the loop
