@@ -795,9 +795,13 @@ void fwd_kernel(const FwdParams p) {
           if (act) {
             __builtin_amdgcn_sched_barrier(0);
             score_tile(kt, s, tw, std::true_type{});
+            if constexpr (!NZ) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
-            sched_score_tile<KS, 8>();
+              for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
+              sched_score_tile<KS, 8>();
+            } else {
+              sched_score_tile<KS, 0>();
+            }
           } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
@@ -813,14 +817,19 @@ void fwd_kernel(const FwdParams p) {
           update_offset_of(s);
           u32x4 pb[4];
           l_i += make_p(s, pb);
-          if constexpr (ST) {
+          if constexpr (ST && !NZ) {
             // Keep the stored tiles' registers until the weights are formed.
 #pragma unroll
             for (int i = 0; i < 8; ++i) asm volatile("" ::"v"(w[i]));
           }
           pv_mma(pb, vt);
           if constexpr (ST) {
-            zero_batch();
+            if constexpr (NZ) {
+#pragma unroll
+              for (int i = 0; i < 8; ++i) buf_store16_nt(w[i], rs, o[i]);
+            } else {
+              zero_batch();
+            }
             interleave_mfma_stores<kZero>();
           }
         } else if constexpr (ST) {
@@ -1017,7 +1026,7 @@ void fwd_kernel(const FwdParams p) {
     if (storer) {
       // (Packed GQA writers keep one storer copy: their registers have no
       // room for a second.)
-      if constexpr (kMid || PACK) {
+      if constexpr (PACK) {
         main_loop(std::true_type{}, std::false_type{});
       } else {
         if (zr.pending())
