@@ -177,6 +177,34 @@ def test_scores_config2_shape(gpu):
     assert_scores_close(scores[:, sel], ref["scores"])
 
 
+# The multi-round score writers with no causal mask: every workgroup writes
+# score tiles only (no zeros), so the storer waves run their copy of the key
+# loop that stores between the O += P V MFMAs.  B*H*ceil(M/256) > 256
+# workgroups selects the 8-wave 256-row writer; 4 heads are checked against
+# the oracle, every head's row sums against attention_with_row_sum.
+@pytest.mark.parametrize("shape,dtype", [
+    ((1, 80, 80, 1024, 1024, 128), torch.float16),
+    ((2, 48, 48, 700, 520, 64), torch.bfloat16),
+], ids=["B1H80S1024D128f16", "B2H48M700N520D64bf16"])
+def test_scores_noncausal_multi_round(shape, dtype, gpu):
+    B, Hq, Hk, M, N, D = shape
+    print(f"[case] scores non-causal multi-round {_label(shape)} {dtype}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=6)
+    qd, kd, vd = q.to(gpu), k.to(gpu), v.to(gpu)
+    out, scores = fas.attention_with_scores(qd, kd, vd, causal=False)
+    _, row = fas.attention_with_row_sum(qd, kd, vd, causal=False)
+    torch.cuda.synchronize()
+    # Sums of the stored (rounded) scores: bf16 keeps 8 significant bits.
+    rs = scores.float().sum(-1)
+    tol = 2e-3 if dtype == torch.float16 else 1e-2
+    assert ((rs - row).abs().max() / row.abs().max()).item() < tol
+    sel = [0, 7, Hq // 2 + 1, Hq - 1]
+    ref = naive.reference_forward(q[-1:, sel], k[-1:, sel], v[-1:, sel], causal=False,
+                                  want=("out", "scores"))
+    assert_out_close(out[-1:, sel], ref["out"])
+    assert_scores_close(scores[-1:, sel], ref["scores"])
+
+
 def test_noncontiguous_inputs(gpu):
     """(B, S, H, D) storage viewed as (B, H, S, D): strides are honoured."""
     B, H, S, D = 1, 4, 192, 64
