@@ -131,6 +131,35 @@ def test_explicit_sm_scale(ep, sm_scale, gpu):
          sm_scale=sm_scale)
 
 
+@pytest.mark.parametrize("sm_scale", [1.0, 1.5, -3.0], ids=["one", "1.5", "neg3"])
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_scores_scale_above_one(sm_scale, causal, dtype, gpu):
+    """sm_scale at and above 1 (and negative): the writer scales each score
+    in fp32 after the q . k product, never q itself."""
+    _run("attention_with_scores", (1, 4, 2, 192, 320, 64), dtype, causal, gpu, seed=13,
+         sm_scale=sm_scale)
+
+
+def test_scores_q_times_scale_past_fp16_range(gpu):
+    """fp16 |q| up to ~4500 with sm_scale 100: q * sm_scale lies past the
+    fp16 range (65504) while the scaled scores (k is tiny) stay near +-1000;
+    scores and output match the oracle (the writer must not form
+    q * sm_scale in the input type)."""
+    dtype = torch.float16
+    B, Hq, Hk, M, N, D = 1, 2, 1, 130, 200, 64
+    print(f"[case] attention_with_scores q*scale past fp16 range {dtype}", flush=True)
+    q, k, v = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=torch.float32, seed=21)
+    q, k, v = (q * 1000.0).to(dtype), (k * 0.001).to(dtype), v.to(dtype)
+    out, scores = fas.attention_with_scores(q.to(gpu), k.to(gpu), v.to(gpu), causal=True,
+                                            sm_scale=100.0)
+    torch.cuda.synchronize()
+    ref = naive.reference_forward(q, k, v, causal=True, sm_scale=100.0, want=("out", "scores"))
+    assert torch.isfinite(scores.float()).all()
+    assert_out_close(out, ref["out"])
+    assert_scores_close(scores, ref["scores"])
+
+
 @pytest.mark.parametrize("ep", PLAIN_EPS + ["attention_cross_token_softmax_sum"])
 def test_large_magnitude_inputs(ep, gpu):
     """q, k, v ~ N(0, 6^2): base-2 exponents spread over hundreds, so the row
