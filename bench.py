@@ -115,8 +115,11 @@ def work(name: str, B, H, Hk, M, N, D, causal, split, elem=2):
         return 4 * B * H * D * P, qkvo + 4 * B * Hk * split
     if name == "cross_softmax":
         return 4 * B * H * D * P + 2 * B * H * D * Px, qkvo + 4 * B * Hk * split
-    # buffered: pass 2 reloads the region's fp32 scores instead of recomputing
-    region = 4 * B * H * max(M - split, 0) * split
+    # buffered: pass 2 reloads the region instead of recomputing its scores.
+    # The region leaves pass 1 as fp16 exponents (2 bytes a score) plus one
+    # fp32 offset per row and 64-key tile, written once and read once (the
+    # reference's raw fp32 scores would be twice the bytes).
+    region = B * H * max(M - split, 0) * (2 * split + 4 * ((split + 63) // 64))
     return 4 * B * H * D * P, qkvo + 2 * region + 4 * B * Hk * split
 
 

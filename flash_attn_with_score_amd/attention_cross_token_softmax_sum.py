@@ -24,13 +24,15 @@ def attention_cross_token_softmax_sum_buffered(
     sm_scale: float = None,
     dropout_p: float = 0.0,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Same result as attention_cross_token_softmax_sum; pass 1 stores the fp32
-    raw scores of the region (queries >= split, keys < split) in a scratch
-    buffer and pass 2 reloads them instead of recomputing q . k.
+    """Same result as attention_cross_token_softmax_sum; pass 1 stores the
+    scores of the region (queries >= split, keys < split) in a scratch buffer
+    and pass 2 reloads them instead of recomputing q . k.
 
-    The scratch is B * Hq * max(M - split, 0) * split * 4 bytes (only the
-    region is ever re-read), where the reference allocates
-    B * Hq * M * N * 4 (:704-705).
+    The scratch holds only the region (the only part ever re-read; the
+    reference allocates B * Hq * M * N * 4 bytes of raw fp32 scores,
+    :704-705), each score as an fp16 base-2 exponent relative to its row's
+    maximum over the region keys of its 64-key tile, plus those maxima:
+    B * Hq * max(M - split, 0) * (split * 2 + ceil(split / 64) * 4) bytes.
     """
     Dq, Dk, Dv = q.shape[-1], k.shape[-1], v.shape[-1]
     assert Dq == Dk == Dv, "Q, K, V must have the same head_dim"

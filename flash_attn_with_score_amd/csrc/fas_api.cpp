@@ -369,7 +369,7 @@ ColPlan col_plan(const Problem& pr, bool buffered, int64_t ncols, bool fold_head
 }
 
 struct Workspace {
-  size_t lse = 0, part = 0, bsum = 0, region = 0, total = 0;  // byte offsets / total
+  size_t lse = 0, part = 0, bsum = 0, region = 0, region_m = 0, total = 0;  // byte offsets / total
   size_t ticket = 0;                                            // column-pass tickets
   ColPlan cp;                                                   // column-pass head split
   size_t bits = 0;                                              // dropout keep bits
@@ -560,10 +560,14 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
     }
   }
   if (variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED) {
+    // The region's fp16 exponents, then one fp32 offset per row and 64-key
+    // tile.
     w.has_region = true;
     w.region = off;
     const int64_t rows = pr.M > split ? pr.M - split : 0;
-    off += align256((size_t)pr.B * pr.H * rows * split * 4);
+    off += align256((size_t)pr.B * pr.H * rows * split * 2);
+    w.region_m = off;
+    off += align256((size_t)pr.B * pr.H * rows * ((split + 63) / 64) * 4);
   }
   if (variant == FAS_VARIANT_ATTENTION_BACKWARD) {
     const size_t rows = (size_t)pr.B * pr.H * bwd_mpad(pr) * 4;
@@ -733,9 +737,11 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   }
   if (!buffered) apply_split(p, w, ws);
   if (buffered) {
-    p.region = at<float>(ws, w.region);
+    p.region = at<uint16_t>(ws, w.region);
+    p.region_m = at<float>(ws, w.region_m);
+    p.region_nt = (int)((split + 63) / 64);
     p.split = (int)split;
-    p.vec_region = (split % 4 == 0) ? 1 : 0;
+    p.vec_region = (split % 8 == 0) ? 1 : 0;
   }
   const int mode = buffered ? fas::kFwdRegion : w.has_bits ? fas::kFwdPlainKeepBits : fas::kFwdPlain;
   if ((rc = run_fwd(fn, p, pr, mode, stream))) return rc;
@@ -747,6 +753,8 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   c.k = p.k;
   c.lse2 = p.lse2;
   c.region = p.region;
+  c.region_m = p.region_m;
+  c.region_nt = p.region_nt;
   c.sq0 = p.sq0; c.sq1 = p.sq1; c.sq2 = p.sq2;
   c.sk0 = p.sk0; c.sk1 = p.sk1; c.sk2 = p.sk2;
   c.q_bytes = p.q_bytes;

@@ -11,9 +11,11 @@
 //               computed causal upper triangle, written as zeros
 //   kFwdRowSum  + per-row sum of masked scaled scores
 //               (attention_with_row_sum.py:146-156)
-//   kFwdRegion  + raw fp32 scores of the region rows >= split, keys < split
-//               (masked -> -inf), the first pass of the buffered cross-token
-//               softmax sum (attention_cross_token_softmax_sum.py:539-552)
+//   kFwdRegion  + the scores of the region rows >= split, keys < split, the
+//               first pass of the buffered cross-token softmax sum
+//               (attention_cross_token_softmax_sum.py:539-552), as fp16
+//               base-2 exponents relative to a per-row, per-tile maximum
+//               (masked -> -inf)
 //   kFwdPlainKeepBits
 //               kFwdPlain with dropout, + the keep decisions as bits for the
 //               softmax column pass (which then need not evaluate Philox)
@@ -228,8 +230,8 @@ __device__ __forceinline__ void sched_score_tile() {
 // LDS of the region mode's row-major staging (kFwdRegion only: other
 // instances never instantiate these, so their LDS holds none of it).
 template <int NW>
-__device__ __forceinline__ f32x4* region_stage() {
-  __shared__ __attribute__((aligned(16))) f32x4 a[NW * 512];
+__device__ __forceinline__ u32x4* region_stage() {
+  __shared__ __attribute__((aligned(16))) u32x4 a[NW * 256];
   return a;
 }
 template <int BM>
@@ -298,12 +300,12 @@ void fwd_kernel(const FwdParams p) {
   __shared__ __attribute__((aligned(16))) KvLds kv_lds;
   auto& kv = kv_lds.t;
   __shared__ __attribute__((aligned(16))) u32x4 stg[SG];
-  // Region tiles (kFwdRegion) leave through LDS too: a wave's 32 x 64 fp32
-  // tile (8 KiB, 16-byte chunks XOR-swizzled by row) is read back row-major,
-  // so each store writes four whole 256-byte row segments; rofs holds each
-  // virtual row's element offset in the region (-1 outside it).
+  // Region tiles (kFwdRegion) leave through LDS too: a wave's 32 x 64 fp16
+  // tile (4 KiB, 16-byte chunks XOR-swizzled by row) is read back row-major,
+  // so each store writes eight whole 128-byte row pieces; rofs holds each
+  // virtual row's row index in the region (-1 outside it).
   constexpr bool kRegion = MODE == kFwdRegion;
-  f32x4* rstg = nullptr;
+  u32x4* rstg = nullptr;
   int64_t* rofs = nullptr;
   if constexpr (kRegion) {
     rstg = region_stage<NW>();
@@ -742,7 +744,7 @@ void fwd_kernel(const FwdParams p) {
       const int v = row0 + tid, pos = v / pack;
       const int head = h0 + (v - pos * pack);
       rofs[tid] = pos >= p.split && pos < p.M
-                      ? ((int64_t)(b * p.H + head) * (p.M - p.split) + (pos - p.split)) * p.split
+                      ? (int64_t)(b * p.H + head) * (p.M - p.split) + (pos - p.split)
                       : -1;
     }
   }
@@ -905,45 +907,74 @@ void fwd_kernel(const FwdParams p) {
           rsum += t[0];
         }
         if constexpr (MODE == kFwdRegion) {
-          if (p.vec_region) {
-            if (wave_region && k0 < p.split) {
-              // Stage in the MFMA layout: lane (c, g) holds row c, keys
-              // 32 kb + 16 hf + 8 g + (0..7) = chunks 8 kb + 4 hf + 2 g + u.
-              f32x4* tile = &rstg[wave * 512];
-              __builtin_amdgcn_wave_barrier();
+          if (wave_region && k0 < p.split) {
+            // t: the row's maximum over the tile's region keys (keys past
+            // split masked out of it); the region keeps y = (s - t) * qk_scale
+            // in fp16 (<= 0, near 0 for the weights that matter) and t *
+            // qk_scale per row and tile (0 when every region key is masked,
+            // whose y are then -inf).
+            float mx = neg_inf();
+            if (k0 + BN <= p.split) {
 #pragma unroll
               for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                for (int hf = 0; hf < 2; ++hf)
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+            } else {
 #pragma unroll
-                  for (int u = 0; u < 2; ++u) {
-                    const int ch = 8 * kb + 4 * hf + 2 * g + u, r0 = 8 * hf + 4 * u;
-                    tile[c * 16 + (ch ^ (c & 15))] =
-                        f32x4{s[kb][r0], s[kb][r0 + 1], s[kb][r0 + 2], s[kb][r0 + 3]};
-                  }
-              __builtin_amdgcn_wave_barrier();
-              // Row-major read-back: lane l takes chunk l % 16 of rows
-              // 4 i + l / 16; keys past split are not stored.
-              const int ch = lane & 15, key = k0 + 4 * ch;
+              for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-              for (int i = 0; i < 8; ++i) {
-                const int R = 4 * i + (lane >> 4);
-                const f32x4 val = tile[R * 16 + (ch ^ (R & 15))];
-                const int64_t off = rofs[32 * wave + R];
-                if (off >= 0 && key < p.split)
-                  __builtin_nontemporal_store(val, reinterpret_cast<f32x4*>(p.region + off + key));
-              }
+                for (int r = 0; r < 16; ++r)
+                  if (k0 + 32 * kb + acc_row(r, g) < p.split) mx = fmaxf(mx, s[kb][r]);
             }
-          } else if (qpos >= p.split && row_ok && k0 < p.split) {
-            float* brow = p.region + ((int64_t)bh * (p.M - p.split) + (qpos - p.split)) * p.split;
+            mx = xor32_max(mx);
+            const float mt = mx == neg_inf() ? 0.f : mx * p.qk_scale;
+            const int tile = k0 / BN;
+            if (g == 0) {
+              const int64_t r = rofs[32 * wave + c];
+              if (r >= 0) p.region_m[r * p.region_nt + tile] = mt;
+            }
+            if (p.vec_region) {
+              // Staged like a score tile (row c, 16-byte chunk 4 kb + 2 hf + g
+              // at unit c * 8 + (chunk ^ ((c >> 1) & 7))) and read back
+              // row-major: each store writes eight whole 128-byte row pieces.
+              u32x4* tile_u = &rstg[wave * 256];
+              __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const f32x16& sv = s[j >> 1];
-              const int r0 = 8 * (j & 1);
-              const int key0 = k0 + 16 * j + 8 * g;
+              for (int j = 0; j < 4; ++j) {
+                const f32x16& x = s[j >> 1];
+                const int r0 = 8 * (j & 1);
+                float y[8];
 #pragma unroll
-              for (int e = 0; e < 8; ++e)
-                if (key0 + e < p.split) brow[key0 + e] = sv[r0 + e];
+                for (int e = 0; e < 8; ++e) y[e] = fmaf(x[r0 + e], p.qk_scale, -mt);
+                tile_u[c * 8 + ((2 * j + g) ^ ((c >> 1) & 7))] =
+                    u32x4{F16::pack(y[0], y[1]), F16::pack(y[2], y[3]), F16::pack(y[4], y[5]),
+                          F16::pack(y[6], y[7])};
+              }
+              __builtin_amdgcn_wave_barrier();
+              // Lane l takes chunk l % 8 (keys k0 + 8 (l % 8) .. + 7) of rows
+              // 8 i + l / 8; chunks past split are not stored (split % 8 == 0).
+              const int ch = lane & 7, key = k0 + 8 * ch;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int R = 8 * i + (lane >> 3);
+                const u32x4 val = tile_u[R * 8 + (ch ^ ((R >> 1) & 7))];
+                const int64_t r = rofs[32 * wave + R];
+                if (r >= 0 && key < p.split)
+                  __builtin_nontemporal_store(
+                      val, reinterpret_cast<u32x4*>(p.region + r * p.split + key));
+              }
+            } else if (qpos >= p.split && row_ok) {
+              uint16_t* brow =
+                  p.region + ((int64_t)bh * (p.M - p.split) + (qpos - p.split)) * p.split;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const f32x16& sv = s[j >> 1];
+                const int r0 = 8 * (j & 1);
+                const int key0 = k0 + 16 * j + 8 * g;
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                  if (key0 + e < p.split) brow[key0 + e] = F16::cvt(fmaf(sv[r0 + e], p.qk_scale, -mt));
+              }
             }
           }
         }

@@ -53,7 +53,13 @@ struct FwdParams {
   float* lse_ln;     // optional (B,H,M) strided: m*sm_scale + ln(l), -inf for empty rows
   uint16_t* scores;  // kFwdScores
   float* aux;        // kFwdRowSum: (B,H,M) strided
-  float* region;     // kFwdRegion: (B*H, M - split, split) contiguous fp32
+  // kFwdRegion: the region (rows >= split, keys < split) as fp16 base-2
+  // exponents y = (s - t) * qk_scale relative to t, the row's maximum over
+  // the region keys of its 64-key tile: region (B*H, M - split, split)
+  // contiguous, region_m (B*H, M - split, region_nt) the t * qk_scale.
+  uint16_t* region;
+  float* region_m;
+  int region_nt;     // 64-key tiles per region row, ceil(split / 64)
   int64_t sq0, sq1, sq2;
   int64_t sk0, sk1, sk2;
   int64_t sv0, sv1, sv2;
@@ -119,7 +125,9 @@ struct ColsmParams {
   const float* lse2;     // (B*H, M) base-2 LSE from the forward pass
   const float* lse_ln;   // or, when set, the natural-log normalizer (B,H,M) strided
   int64_t sl0, sl1, sl2;
-  const float* region;   // buffered source: (B*H, M - split, split) raw fp32 scores
+  const uint16_t* region;  // buffered source: fp16 exponents (FwdParams::region)
+  const float* region_m;   // and their per-row, per-64-key-tile offsets
+  int region_nt;
   float* out;            // (B, H / fold, ncols) strided output
   int64_t sq0, sq1, sq2;
   int64_t sk0, sk1, sk2;

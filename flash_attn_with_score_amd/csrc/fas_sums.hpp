@@ -432,16 +432,19 @@ void colsm64_kernel(const ColsmParams p) {
 }
 #pragma clang diagnostic pop
 
-// Buffered source: pass 1 left the raw fp32 scores of the region (rows >=
-// split, keys < split; masked entries -inf) in p.region.  A workgroup of 4
-// waves owns 256 keys of one output group and walks the query heads of its
+// Buffered source: pass 1 left the region (rows >= split, keys < split) as
+// fp16 base-2 exponents y = (s - t) * qk_scale in p.region and t * qk_scale,
+// t the row's maximum over the region keys of each 64-key tile, in
+// p.region_m, so a weight is exp2(y + t * qk_scale - lse2).  A workgroup of
+// 4 waves owns 256 keys of one output group and walks the query heads of its
 // split one after the other: lane l of every wave holds keys 4 l .. 4 l + 3
-// and reads them as one 16-byte load per row, so a wave reads 1 KiB
-// contiguous per row; the waves take every fourth row (the row and its lse2
-// are wave-uniform, the latter a scalar load), several rows in flight, and
-// their sums meet in LDS in a fixed order.  Entries above a key's first
-// admissible row were never written and are excluded by a select.  VEC:
-// split % 4 == 0 (16-byte aligned rows); otherwise one key per lane.
+// (one 64-key tile) and reads them as one 8-byte load per row, so a wave
+// reads 512 bytes contiguous per row; the waves take every fourth row (the
+// row and its lse2 are wave-uniform, the latter a scalar load), several rows
+// in flight, and their sums meet in LDS in a fixed order.  Entries above a
+// key's first admissible row were never written and are excluded by a
+// select.  VEC: split % 4 == 0 (8-byte aligned lane groups); otherwise one
+// key per lane.
 template <bool VEC>
 __global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p) {
   constexpr int KPL = VEC ? 4 : 1;  // keys per lane
@@ -455,6 +458,7 @@ __global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int key0 = kb * BKB + KPL * lane;
+  const int tile = key0 / 64;  // the lane's keys lie in one 64-key tile
   const int rows = max(0, p.M - p.split);
   // First admissible row of each key, and of the workgroup's first key.
   int rs[KPL];
@@ -467,32 +471,40 @@ __global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p
   for (int e = 0; e < KPL; ++e) acc[e] = 0.f;
   for (int h = ho * p.fold + item.sp; h < (ho + 1) * p.fold; h += p.nsplit) {
     const int64_t bh = (int64_t)b * p.H + h;
-    const float* reg = p.region + bh * rows * p.split;
+    const uint16_t* reg = p.region + bh * rows * p.split;
+    const float* rm = p.region_m + bh * rows * p.region_nt;
     const float* lse = p.lse2 + bh * p.M;
     auto row_step = [&](int row) __attribute__((always_inline)) {
       const float l = lse[row];
-      const float* rp = reg + (int64_t)(row - p.split) * p.split + key0;
+      const int64_t rr = row - p.split;
+      const uint16_t* rp = reg + rr * p.split + key0;
+      const float off = (live ? rm[rr * p.region_nt + tile] : 0.f) - l;
       float v[KPL];
       if constexpr (VEC) {
-        const f32x4 x = live ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(rp))
-                             : f32x4{0.f, 0.f, 0.f, 0.f};
-        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 x = live ? __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(rp))
+                             : u32x2{0u, 0u};
+        v[0] = F16::to_f32((uint16_t)(x.x & 0xffffu));
+        v[1] = F16::to_f32((uint16_t)(x.x >> 16));
+        v[2] = F16::to_f32((uint16_t)(x.y & 0xffffu));
+        v[3] = F16::to_f32((uint16_t)(x.y >> 16));
       } else {
-        v[0] = live ? rp[0] : 0.f;
+        v[0] = live ? F16::to_f32(rp[0]) : 0.f;
       }
 #pragma unroll
       for (int e = 0; e < KPL; ++e) {
-        const float w = exp2f_fast(fmaf(v[e], p.qk_scale, -l));
+        const float w = exp2f_fast(v[e] + off);
         acc[e] += row >= rs[e] ? w : 0.f;
       }
     };
+    // Eight rows in flight per wave: the pass is bound by load latency
+    // where a workgroup has few rows (metric shape, split 3072: 71.1 us at
+    // four rows in flight).
     int row = __builtin_amdgcn_readfirstlane(r_lo + wave);
 #pragma unroll 1
-    for (; row + 12 < p.M; row += 16) {
-      row_step(row);
-      row_step(row + 4);
-      row_step(row + 8);
-      row_step(row + 12);
+    for (; row + 28 < p.M; row += 32) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) row_step(row + 4 * u);
     }
     for (; row < p.M; row += 4) row_step(row);
   }

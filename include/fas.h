@@ -221,11 +221,13 @@ int fas_attention_cross_token_softmax_sum(const fas_attn_args* a, int64_t split,
 
 /* Replaces attention_cross_token_softmax_sum.py:639-732 (+ buffered kernel
  * :434-636): same output as fas_attention_cross_token_softmax_sum, but the
- * first pass stores the raw fp32 scores of the region (rows >= split, keys
- * < split) in the workspace and the second pass reloads them instead of
- * recomputing q.k.  The reference sizes its buffer B*Hq*M*N*4 bytes
- * (attention_cross_token_softmax_sum.py:704-705); only the region,
- * B*Hq*(M - split)*split*4 bytes, is ever re-read, so only it is kept. */
+ * first pass stores the scores of the region (rows >= split, keys < split)
+ * in the workspace and the second pass reloads them instead of recomputing
+ * q.k.  The reference keeps raw fp32 scores in a B*Hq*M*N*4-byte buffer
+ * (attention_cross_token_softmax_sum.py:704-705); only the region is ever
+ * re-read, so only it is kept, as fp16 base-2 exponents relative to each
+ * row's maximum over the region keys of a 64-key tile plus that maximum:
+ * B*Hq*(M - split)*(split*2 + ceil(split/64)*4) bytes. */
 int fas_attention_cross_token_softmax_sum_buffered(const fas_attn_args* a, int64_t split,
                                                    float* cross, const int64_t cross_stride[3],
                                                    void* workspace, size_t workspace_bytes,

@@ -160,7 +160,8 @@ def test_scores_q_times_scale_past_fp16_range(gpu):
     assert_scores_close(scores, ref["scores"])
 
 
-@pytest.mark.parametrize("ep", PLAIN_EPS + ["attention_cross_token_softmax_sum"])
+@pytest.mark.parametrize("ep", PLAIN_EPS + ["attention_cross_token_softmax_sum",
+                                          "attention_cross_token_softmax_sum_buffered"])
 def test_large_magnitude_inputs(ep, gpu):
     """q, k, v ~ N(0, 6^2): base-2 exponents spread over hundreds, so the row
     maxima of the two half-waves that share a query row differ widely.  A
