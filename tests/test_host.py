@@ -145,8 +145,11 @@ def test_workspace_sizes(lib):
     assert ws(_native.VARIANT_SOFTMAX_COL_SUM) == r256(B * Hq * M * 4) + folds(N, False)
     assert ws(_native.VARIANT_CROSS_QK_SUM) == r256(B * Hk * ((M - split + 63) // 64 + 1) * D * 4)
     assert ws(_native.VARIANT_CROSS_SOFTMAX_SUM) == r256(B * Hq * M * 4) + folds(split, False)
+    # The buffered region: fp16 exponents, then one fp32 offset per row and
+    # 64-key tile.
     assert ws(_native.VARIANT_CROSS_SOFTMAX_SUM_BUFFERED) == (
-        r256(B * Hq * M * 4) + folds(split, True) + r256(B * Hq * (M - split) * split * 4))
+        r256(B * Hq * M * 4) + folds(split, True) + r256(B * Hq * (M - split) * split * 2)
+        + r256(B * Hq * (M - split) * ((split + 63) // 64) * 4))
     # MHA needs no per-query-head partials.
     a1 = make_args(B, 4, 4, M, N, D)
     assert lib.fas_workspace_bytes(_native.VARIANT_SOFTMAX_COL_SUM, ctypes.byref(a1), 0) == \
