@@ -560,8 +560,8 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
     }
   }
   if (variant == FAS_VARIANT_CROSS_SOFTMAX_SUM_BUFFERED) {
-    // The region's fp16 exponents, then one fp32 offset per row and 64-key
-    // tile.
+    // The region's fp16 exponents, then one fp32 offset per 64-key tile and
+    // region row (tile-major).
     w.has_region = true;
     w.region = off;
     const int64_t rows = pr.M > split ? pr.M - split : 0;
@@ -739,7 +739,7 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   if (buffered) {
     p.region = at<uint16_t>(ws, w.region);
     p.region_m = at<float>(ws, w.region_m);
-    p.region_nt = (int)((split + 63) / 64);
+    p.region_rows = (int64_t)pr.B * pr.H * (pr.M > split ? pr.M - split : 0);
     p.split = (int)split;
     p.vec_region = (split % 8 == 0) ? 1 : 0;
   }
@@ -754,7 +754,7 @@ int run_softmax(const char* fn, int variant, const fas_attn_args* a, int64_t spl
   c.lse2 = p.lse2;
   c.region = p.region;
   c.region_m = p.region_m;
-  c.region_nt = p.region_nt;
+  c.region_rows = p.region_rows;
   c.sq0 = p.sq0; c.sq1 = p.sq1; c.sq2 = p.sq2;
   c.sk0 = p.sk0; c.sk1 = p.sk1; c.sk2 = p.sk2;
   c.q_bytes = p.q_bytes;

@@ -931,7 +931,7 @@ void fwd_kernel(const FwdParams p) {
             const int tile = k0 / BN;
             if (g == 0) {
               const int64_t r = rofs[32 * wave + c];
-              if (r >= 0) p.region_m[r * p.region_nt + tile] = mt;
+              if (r >= 0) p.region_m[tile * p.region_rows + r] = mt;
             }
             if (p.vec_region) {
               // Staged like a score tile (row c, 16-byte chunk 4 kb + 2 hf + g

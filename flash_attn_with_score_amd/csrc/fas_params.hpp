@@ -56,10 +56,11 @@ struct FwdParams {
   // kFwdRegion: the region (rows >= split, keys < split) as fp16 base-2
   // exponents y = (s - t) * qk_scale relative to t, the row's maximum over
   // the region keys of its 64-key tile: region (B*H, M - split, split)
-  // contiguous, region_m (B*H, M - split, region_nt) the t * qk_scale.
+  // contiguous, region_m (ceil(split / 64), region_rows) the t * qk_scale,
+  // tile-major so a wave's rows of one tile are adjacent.
   uint16_t* region;
   float* region_m;
-  int region_nt;     // 64-key tiles per region row, ceil(split / 64)
+  int64_t region_rows;  // B*H*(M - split)
   int64_t sq0, sq1, sq2;
   int64_t sk0, sk1, sk2;
   int64_t sv0, sv1, sv2;
@@ -126,8 +127,8 @@ struct ColsmParams {
   const float* lse_ln;   // or, when set, the natural-log normalizer (B,H,M) strided
   int64_t sl0, sl1, sl2;
   const uint16_t* region;  // buffered source: fp16 exponents (FwdParams::region)
-  const float* region_m;   // and their per-row, per-64-key-tile offsets
-  int region_nt;
+  const float* region_m;   // and their per-64-key-tile, per-row offsets
+  int64_t region_rows;
   float* out;            // (B, H / fold, ncols) strided output
   int64_t sq0, sq1, sq2;
   int64_t sk0, sk1, sk2;

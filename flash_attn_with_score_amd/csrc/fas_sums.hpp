@@ -472,13 +472,13 @@ __global__ __launch_bounds__(256) void colsm_buffered_kernel(const ColsmParams p
   for (int h = ho * p.fold + item.sp; h < (ho + 1) * p.fold; h += p.nsplit) {
     const int64_t bh = (int64_t)b * p.H + h;
     const uint16_t* reg = p.region + bh * rows * p.split;
-    const float* rm = p.region_m + bh * rows * p.region_nt;
+    const float* rm = p.region_m + tile * p.region_rows + bh * rows;
     const float* lse = p.lse2 + bh * p.M;
     auto row_step = [&](int row) __attribute__((always_inline)) {
       const float l = lse[row];
       const int64_t rr = row - p.split;
       const uint16_t* rp = reg + rr * p.split + key0;
-      const float off = (live ? rm[rr * p.region_nt + tile] : 0.f) - l;
+      const float off = (live ? rm[rr] : 0.f) - l;
       float v[KPL];
       if constexpr (VEC) {
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
