@@ -268,6 +268,29 @@ def time_steps(call, steps: int, warmup: int, prewarm_ms: float):
     return wall, dev_ms, warm
 
 
+def time_cold(call, reps: int, flush_bytes: int = 512 << 20) -> float:
+    """Average device time of `reps` calls, each timed alone with HIP events
+    on torch's current stream right after a read of `flush_bytes` (outside
+    the events) that evicts the XCDs' L2 caches and the 256 MB Infinity Cache,
+    so every call reads its inputs from HBM.  A read, not a write: a written
+    flush leaves up to 256 MB of dirty lines that the timed call would then
+    pay to write back."""
+    buf = torch.ones(flush_bytes // 4, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    events = []
+    for _ in range(reps):
+        buf.amax()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        call()
+        end.record(stream)
+        events.append((start, end))
+    torch.cuda.synchronize()
+    del buf
+    return sum(a.elapsed_time(b) for a, b in events) / reps
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -349,6 +372,11 @@ def main() -> int:
     if traffic is not None:
         roof["traffic_source"] = source
     roof["kernel_ms"] = round(dev_ms, 4)
+    if bound == "hbm":
+        # The same calls with the caches evicted before each one.
+        cold_ms = time_cold(call, 20)
+        roof["kernel_ms_cold"] = round(cold_ms, 4)
+        roof["frac_cold"] = round(nbytes / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)
     roof["algorithmic_bytes"] = nbytes
     roof["algorithmic_flop"] = flop
 
