@@ -176,6 +176,7 @@ struct RawParams {
   int ncols;
   int causal, causal_off;
   int nextra;            // causal: key blocks below causal_off (all rows admissible)
+  int kgroups;           // full sums: 64-key groups per workgroup (set by the launcher)
   float sm_scale;        // signed
 };
 

@@ -60,8 +60,13 @@ static hipError_t rawsum_t(const RawParams& p, bool suffix, hipStream_t s) {
     const unsigned nw = (unsigned)((p.M + 63) / 64 + p.nextra);
     if (nw > 0) hipLaunchKernelGGL((colraw_kernel<E, D, true>), dim3(nw, bhk), dim3(256), 0, s, p);
   } else {
-    const unsigned nw = (unsigned)((p.ncols + 63) / 64);
-    if (nw > 0) hipLaunchKernelGGL((colraw_kernel<E, D, false>), dim3(nw, bhk), dim3(256), 0, s, p);
+    // Up to 8 groups of 64 keys per workgroup while at least 512
+    // workgroups (two per CU) remain.
+    const int64_t groups = (p.ncols + 63) / 64;
+    RawParams q = p;
+    q.kgroups = (int)std::max<int64_t>(1, std::min<int64_t>(8, groups * bhk / 512));
+    const unsigned nw = (unsigned)((groups + q.kgroups - 1) / q.kgroups);
+    if (nw > 0) hipLaunchKernelGGL((colraw_kernel<E, D, false>), dim3(nw, bhk), dim3(256), 0, s, q);
   }
   return hipGetLastError();
 }

@@ -613,7 +613,10 @@ __device__ __forceinline__ float key_dot(const RawParams& p, const uint16_t* kba
 // Causal column sums: workgroup w < nextra handles keys [64w, 64w+64) below
 // causal_off (every row admissible); the others own one 64-row block rb and
 // the keys j = row + causal_off of its rows.  Non-causal / cross: every
-// workgroup owns 64 keys and uses the total.
+// workgroup owns p.kgroups groups of 64 keys and uses the total, which it
+// sums from the head's block sums once for all of them (one group per
+// workgroup re-read the whole block-sum table per 64 keys: at B2 H32 S8192
+// four times the bytes of K from the L2).
 template <class E, int D, bool SUFFIX>
 __global__ __launch_bounds__(256) void colraw_kernel(const RawParams p) {
   __shared__ float vec[64][D];
@@ -629,11 +632,14 @@ __global__ __launch_bounds__(256) void colraw_kernel(const RawParams p) {
   if (!SUFFIX || w < p.nextra) {
     // Keys every query row sees: the sum over all row blocks.
     block_range_sum<D>(bs, 0, p.nblk, vec[0], scratch);
-    const int key = 64 * w + kslot;
     const int lim = SUFFIX ? min(p.ncols, p.causal_off) : p.ncols;
-    if (key < lim) {
-      const float dot = key_dot<E, D>(p, kbase, key, vec[0], part);
-      if (part == 0) p.out[b * p.so0 + hk * p.so1 + (int64_t)key * p.so2] = dot * p.sm_scale;
+    const int ng = SUFFIX ? 1 : p.kgroups;
+    for (int kg = 0; kg < ng; ++kg) {
+      const int key = 64 * (w * ng + kg) + kslot;
+      if (key < lim) {
+        const float dot = key_dot<E, D>(p, kbase, key, vec[0], part);
+        if (part == 0) p.out[b * p.so0 + hk * p.so1 + (int64_t)key * p.so2] = dot * p.sm_scale;
+      }
     }
     return;
   }
