@@ -539,11 +539,26 @@ __global__ __launch_bounds__(256) void qsum_blocks_kernel(const RawParams p) {
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   const int r0 = p.row_lo + 64 * blk;
   const int r1 = min(p.M, r0 + 64);
-  for (int gg = 0; gg < p.G; ++gg) {
-    const uint16_t* qh = p.q + b * p.sq0 + (int64_t)(hk * p.G + gg) * p.sq1 + ch * 8;
-    for (int row = r0 + rg; row < r1; row += RPI) {
+  // Items (head gg, row r0 + rg + RPI j) in head-major order, four loads in
+  // flight (a GQA group's G heads are G times the rows of one workgroup),
+  // added in item order.
+  constexpr int ITER = (64 + RPI - 1) / RPI;
+  const int nitems = p.G * ITER;
+  const uint16_t* qb = p.q + b * p.sq0 + (int64_t)(hk * p.G) * p.sq1 + ch * 8;
+  auto load_item = [&](int i) __attribute__((always_inline)) {
+    const int gg = i / ITER, row = r0 + rg + RPI * (i - gg * ITER);
+    return i < nitems && row < r1
+               ? *reinterpret_cast<const u32x4*>(qb + (int64_t)gg * p.sq1 + (int64_t)row * p.sq2)
+               : u32x4{0u, 0u, 0u, 0u};
+  };
+  for (int i = 0; i < nitems; i += 4) {
+    u32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = load_item(i + u);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
       float x[8];
-      unpack8<E>(*reinterpret_cast<const u32x4*>(qh + (int64_t)row * p.sq2), x);
+      unpack8<E>(v[u], x);
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[e] += x[e];
     }
