@@ -912,6 +912,18 @@ static int run_scores(const char* fn, const fas_attn_args* a, const Problem& pr,
                   pr.N % 8 == 0
               ? 1
               : 0;
+  // Up to 256 query rows with 16-byte score stores: the resident-Q kernel,
+  // one workgroup per CU, each walking two or more of its head's 512-key
+  // blocks.
+  if (p.vec && pr.M <= fas::kScoresResidentRows) {
+    const int64_t nkb = (pr.N + fas::kScoresResidentKeys - 1) / fas::kScoresResidentKeys;
+    const int64_t heads = (int64_t)pr.B * pr.H;
+    const int64_t ngrp = std::min<int64_t>(nkb, (device_cu_count() + heads - 1) / heads);
+    if (nkb >= 2 * ngrp) {
+      p.ngrp = (int)ngrp;
+      p.nkb = (int)nkb;
+    }
+  }
   p.sm_scale = pr.sm_scale;
   return hip_status(fn, fas::launch_scores(p, pr.dtype, pr.D, static_cast<hipStream_t>(stream)));
 }

@@ -27,6 +27,10 @@ constexpr int kBwdBlock = 128;
 hipError_t launch_scores(const ScoresParams& p, int dtype, int d, hipStream_t s);
 // Keys per scores-only workgroup (4 key groups x 64 keys).
 constexpr int kScoresKeysPerBlock = 256;
+// Most query rows, and keys per block, of the resident-Q scores kernel
+// (ScoresParams::ngrp > 0).
+constexpr int kScoresResidentRows = 256;
+constexpr int kScoresResidentKeys = 512;
 
 hipError_t launch_fill_zero(float* p, int64_t s0, int64_t s1, int64_t s2, int64_t n0, int64_t n1,
                             int64_t n2, hipStream_t s);

@@ -274,9 +274,10 @@ struct ScoresParams {
   int B, H, G, M, N;
   int mask;           // 1: causal / key-range mask, masked entries written as 0
   int causal_off;     // key j admissible for query i iff causal_off + i >= j
-  int nkb;            // 256-key blocks
+  int nkb;            // 256-key blocks (512-key blocks for the resident-Q kernel)
   int nrs;            // row ranges per key block
   int spr;            // 64-row steps per row range
+  int ngrp;           // > 0: resident-Q kernel with ngrp workgroups per head (M <= 256)
   int vec;            // base and row strides 16-byte aligned, N % 8 == 0: 16-byte stores
   float sm_scale;     // signed
 };

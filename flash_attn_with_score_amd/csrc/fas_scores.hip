@@ -3,20 +3,51 @@
 #include "fas_scores.hpp"
 
 static_assert(fas::kScoresKeysPerBlock == fas::kScoresKeys, "host and kernel key blocks");
+static_assert(fas::kScoresResidentRows == fas::kScoresResRows, "host and kernel resident rows");
+static_assert(fas::kScoresResidentKeys == 64 * fas::kScoresWaves, "host and kernel resident blocks");
 
 namespace fas {
 
+template <class E, int D, bool MASK>
+static void qres_launch(int rows, dim3 g, dim3 b, const ScoresParams& p, hipStream_t s) {
+  if (rows == 32)
+    hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 32>), g, b, 0, s, p);
+  else if (rows == 64)
+    hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 64>), g, b, 0, s, p);
+  else if (rows == 128)
+    hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 128>), g, b, 0, s, p);
+  else
+    hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 256>), g, b, 0, s, p);
+}
+
 template <class E, int D>
 static hipError_t scores_t(const ScoresParams& p, hipStream_t s) {
+  if (p.ngrp > 0) {
+    if (p.M > kScoresResRows || p.ngrp > p.nkb || !p.vec) return hipErrorInvalidValue;
+    const int64_t grid = (int64_t)p.B * p.H * p.ngrp;
+    if (grid > INT32_MAX) return hipErrorInvalidValue;
+    const dim3 g((unsigned)grid), b(64 * kScoresWaves);
+    // Resident rows: the fewest of 32, 64, 128 and 256 that cover M (nkb
+    // counts 512-key blocks).
+    const int rows = p.M <= 32 ? 32 : p.M <= 64 ? 64 : p.M <= 128 ? 128 : 256;
+    if (p.mask)
+      qres_launch<E, D, true>(rows, g, b, p, s);
+    else
+      qres_launch<E, D, false>(rows, g, b, p, s);
+    return hipGetLastError();
+  }
   const int64_t grid = (int64_t)p.B * p.H * p.nkb * p.nrs;
   if (grid > INT32_MAX) return hipErrorInvalidValue;
   if (grid > 0) {
-    if (p.mask)
-      hipLaunchKernelGGL((scores_kernel<E, D, true>), dim3((unsigned)grid), dim3(64 * kScoresWaves),
-                         0, s, p);
+    const dim3 g((unsigned)grid), b(64 * kScoresWaves);
+    if (p.mask && p.vec)
+      hipLaunchKernelGGL((scores_kernel<E, D, true, true>), g, b, 0, s, p);
+    else if (p.mask)
+      hipLaunchKernelGGL((scores_kernel<E, D, true, false>), g, b, 0, s, p);
+    else if (p.vec)
+      hipLaunchKernelGGL((scores_kernel<E, D, false, true>), g, b, 0, s, p);
     else
-      hipLaunchKernelGGL((scores_kernel<E, D, false>), dim3((unsigned)grid), dim3(64 * kScoresWaves),
-                         0, s, p);
+      hipLaunchKernelGGL((scores_kernel<E, D, false, false>), g, b, 0, s, p);
   }
   return hipGetLastError();
 }

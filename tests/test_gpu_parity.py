@@ -314,6 +314,50 @@ def test_compute_attention_scores(shape, dtype, gpu):
 
 
 
+# Short query ranges (M <= 256) over many key blocks: the scores-only
+# kernel keeps each head's Q rows in LDS (32, 64, 128 or 256 rows) and every
+# workgroup walks several 512-key blocks (16-byte stores only).  B*H a
+# multiple of 8 and not (12 heads), GQA, a partial last key block and last
+# step, M = 1, uneven numbers of blocks per workgroup (20 blocks over 8
+# workgroups), and B*H >= 256 (one workgroup per head, 2-4 blocks each) at
+# D 16 to 128.
+RESIDENT_Q_SHAPES = [
+    (1, 32, 32, 256, 8192, 128),
+    (2, 16, 4, 200, 10000, 64),
+    (1, 12, 12, 37, 22600, 128),
+    (1, 16, 8, 100, 16384, 128),
+    (1, 32, 32, 32, 8200, 128),
+    (2, 8, 2, 17, 16384, 64),
+    (8, 32, 8, 1, 2048, 128),
+    (4, 64, 64, 64, 520, 32),
+    (2, 128, 128, 130, 1800, 16),
+]
+
+
+@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES, ids=_label)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_compute_attention_scores_resident_q(shape, dtype, gpu):
+    from flash_attn_with_score_amd.attention_scores import compute_attention_scores
+
+    B, Hq, Hk, M, N, D = shape
+    print(f"[case] compute_attention_scores resident q {_label(shape)} {dtype}", flush=True)
+    q, k, _ = inputs.make_qkv(B, Hq, Hk, M, N, D, dtype=dtype, seed=14)
+    got = compute_attention_scores(q.to(gpu), k.to(gpu))
+    torch.cuda.synchronize()
+    ref = naive.reference_forward(q, k, k, causal=False, want=("scores",))["scores"]
+    assert got.dtype == dtype and got.shape == (B, Hq, M, N)
+    assert_out_close(got, ref, "scores")
+
+
+# attention_with_scores on the same shapes: short query ranges take the
+# key-split forward for O and the masked scores-only kernel (causal: keys
+# past N - M + row written as 0).
+@pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
+@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES[:6], ids=_label)
+def test_scores_short_query_resident_q(shape, causal, gpu):
+    _run("attention_with_scores", shape, torch.float16, causal, gpu, seed=15)
+
+
 # GQA packing: a forward workgroup serves all G query heads of its KV head,
 # its rows interleaving the heads (virtual row = position * G + head).
 # Shapes: group sizes 2, 4, 7 and 8; M not a multiple of the block's
