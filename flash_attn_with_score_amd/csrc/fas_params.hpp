@@ -84,7 +84,7 @@ struct FwdParams {
   int vec_scores;    // scores rows 16-byte aligned and N % 8 == 0
   int zero_self;     // score writer: 1 = a workgroup writes its own row block's zeros
                      // (all workgroups run at once), 0 = its mirror row block's
-  int vec_region;    // split % 4 == 0
+  int vec_region;    // split % 8 == 0
   int key_split2;    // score writer with 128-row blocks: 1 = the 8-wave key-split
                      // instance (wave pairs take the even and odd key tiles)
   int dropout;       // 1: the dropout instances (modes other than kFwdRegion)
