@@ -915,13 +915,28 @@ static int run_scores(const char* fn, const fas_attn_args* a, const Problem& pr,
   // Up to 256 query rows with 16-byte score stores: the resident-Q kernel,
   // one workgroup per CU, each walking two or more of its head's 512-key
   // blocks.
+  // Under GQA a workgroup takes the largest power-of-two share of a KV
+  // head's query heads whose rows fit (K loaded once for all of them), as
+  // long as its q and score offsets stay 31-bit.
   if (p.vec && pr.M <= fas::kScoresResidentRows) {
     const int64_t nkb = (pr.N + fas::kScoresResidentKeys - 1) / fas::kScoresResidentKeys;
-    const int64_t heads = (int64_t)pr.B * pr.H;
-    const int64_t ngrp = std::min<int64_t>(nkb, (device_cu_count() + heads - 1) / heads);
-    if (nkb >= 2 * ngrp) {
+    int pshift = 0;
+    auto fits = [&](int pk) {
+      return pr.G % pk == 0 && (int64_t)pk * pr.M <= fas::kScoresResidentRows &&
+             ((int64_t)(pk - 1) * p.sq1 + (int64_t)pr.M * p.sq2) * 2 < fas::kScoresResidentBytes &&
+             ((int64_t)(pk - 1) * st[1] + (int64_t)(pr.M - 1) * st[2] + fas::kScoresResidentKeys) *
+                     2 <
+                 fas::kScoresResidentBytes;
+    };
+    while (fits(2 << pshift)) ++pshift;
+    const int64_t groups = ((int64_t)pr.B * pr.H) >> pshift;
+    const int64_t ngrp = std::min<int64_t>(nkb, (device_cu_count() + groups - 1) / groups);
+    if (fits(1) && nkb >= 2 * ngrp) {
       p.ngrp = (int)ngrp;
       p.nkb = (int)nkb;
+      p.pshift = pshift;
+      if (pshift > 0)
+        p.q_bytes = (uint32_t)(((int64_t)((1 << pshift) - 1) * p.sq1 + (int64_t)pr.M * p.sq2) * 2);
     }
   }
   p.sm_scale = pr.sm_scale;

@@ -31,6 +31,8 @@ constexpr int kScoresKeysPerBlock = 256;
 // (ScoresParams::ngrp > 0).
 constexpr int kScoresResidentRows = 256;
 constexpr int kScoresResidentKeys = 512;
+// Bound on the resident-Q kernel's q and score offsets within a head group.
+constexpr int64_t kScoresResidentBytes = 0x7ffffff0;
 
 hipError_t launch_fill_zero(float* p, int64_t s0, int64_t s1, int64_t s2, int64_t n0, int64_t n1,
                             int64_t n2, hipStream_t s);

@@ -277,7 +277,11 @@ struct ScoresParams {
   int nkb;            // 256-key blocks (512-key blocks for the resident-Q kernel)
   int nrs;            // row ranges per key block
   int spr;            // 64-row steps per row range
-  int ngrp;           // > 0: resident-Q kernel with ngrp workgroups per head (M <= 256)
+  int ngrp;           // > 0: resident-Q kernel with ngrp workgroups per head group
+  // Resident-Q kernel: a group is 2^pshift consecutive query heads of one KV
+  // head (pshift > 0 only under GQA, 2^pshift * M <= 256), its virtual rows
+  // v = m * 2^pshift + j holding position m of head h0 + j.
+  int pshift;
   int vec;            // base and row strides 16-byte aligned, N % 8 == 0: 16-byte stores
   float sm_scale;     // signed
 };

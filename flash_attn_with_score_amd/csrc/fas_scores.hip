@@ -5,6 +5,7 @@
 static_assert(fas::kScoresKeysPerBlock == fas::kScoresKeys, "host and kernel key blocks");
 static_assert(fas::kScoresResidentRows == fas::kScoresResRows, "host and kernel resident rows");
 static_assert(fas::kScoresResidentKeys == 64 * fas::kScoresWaves, "host and kernel resident blocks");
+static_assert(fas::kScoresResidentBytes == fas::kScoresGroupBytes, "host and kernel group extents");
 
 namespace fas {
 
@@ -23,13 +24,17 @@ static void qres_launch(int rows, dim3 g, dim3 b, const ScoresParams& p, hipStre
 template <class E, int D>
 static hipError_t scores_t(const ScoresParams& p, hipStream_t s) {
   if (p.ngrp > 0) {
-    if (p.M > kScoresResRows || p.ngrp > p.nkb || !p.vec) return hipErrorInvalidValue;
-    const int64_t grid = (int64_t)p.B * p.H * p.ngrp;
+    if (p.ngrp > p.nkb || !p.vec) return hipErrorInvalidValue;
+    if (p.pshift < 0 || p.pshift > 3 || p.H % (1 << p.pshift) != 0 ||
+        p.G % (1 << p.pshift) != 0 || (p.M << p.pshift) > kScoresResRows)
+      return hipErrorInvalidValue;
+    const int64_t grid = ((int64_t)p.B * p.H >> p.pshift) * p.ngrp;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
     const dim3 g((unsigned)grid), b(64 * kScoresWaves);
-    // Resident rows: the fewest of 32, 64, 128 and 256 that cover M (nkb
-    // counts 512-key blocks).
-    const int rows = p.M <= 32 ? 32 : p.M <= 64 ? 64 : p.M <= 128 ? 128 : 256;
+    // Resident rows: the fewest of 32, 64, 128 and 256 that cover the
+    // group's 2^pshift * M rows (nkb counts 512-key blocks).
+    const int vr = p.M << p.pshift;
+    const int rows = vr <= 32 ? 32 : vr <= 64 ? 64 : vr <= 128 ? 128 : 256;
     if (p.mask)
       qres_launch<E, D, true>(rows, g, b, p, s);
     else

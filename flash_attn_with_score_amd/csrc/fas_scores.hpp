@@ -38,6 +38,9 @@ namespace fas {
 
 // Byte offset past every buffer extent: the store is dropped.
 constexpr uint32_t kOffNoneScores = 0x80000000u;
+// Extent of a head group's score buffer in the resident-Q kernel: the host
+// keeps every valid store offset below it.
+constexpr uint32_t kScoresGroupBytes = 0x7ffffff0u;
 
 constexpr int kScoresWaves = 8;
 constexpr int kScoresRows = 64;    // query rows per step (2 row groups x 32)
@@ -64,7 +67,10 @@ __device__ __forceinline__ void scores_load_keys(u32x4 (&a0)[D / 16], u32x4 (&a1
 // scaled by sm_scale, masked, converted and stored through the wave's LDS
 // stage st.  VEC_ONLY: the caller runs only with p.vec set (no per-element
 // store path).
-template <class E, int D, bool MASK, bool VEC_ONLY = false>
+// GROUP (the resident-Q kernel): rows are the virtual rows of a head group
+// (2^p.pshift heads from shead on) and every lane's store carries its own
+// validity, past M or N at kOffNoneScores.
+template <class E, int D, bool MASK, bool VEC_ONLY = false, bool GROUP = false>
 __device__ __forceinline__ void scores_tile(const ScoresParams& p, const uint16_t* qt, int qrow,
                                             const u32x4 (&a0)[D / 16], const u32x4 (&a1)[D / 16],
                                             u32x4* st, uint16_t* shead, int wrow0, int k0,
@@ -92,7 +98,8 @@ __device__ __forceinline__ void scores_tile(const ScoresParams& p, const uint16_
     }
   }
   const bool key_ok = k0 + 8 * (lane & 7) < p.N;  // the lane's store unit lies below N
-  const int row = wrow0 + c;  // the lane's query row
+  // The lane's query row (its position within the head for a group).
+  const int row = GROUP ? (wrow0 + c) >> p.pshift : wrow0 + c;
   if (VEC_ONLY || p.vec) {
     // Stage row c, 16-byte unit u = 4j + 2hf + g at c*8 + (u ^ ((c/2) & 7)):
     // conflict-free for these writes (one unit of 32 rows) and for the
@@ -117,21 +124,41 @@ __device__ __forceinline__ void scores_tile(const ScoresParams& p, const uint16_
       }
     __builtin_amdgcn_wave_barrier();
     // Lane l stores unit l % 8 of rows l / 8 + 8i: whole 128-byte runs.
-    // The buffer ends at the wave's last key below N in its last row below
-    // M (row stride >= N), so stores to rows past M drop out.
-    const int nrows = min(32, p.M - wrow0), nkeys = min(64, p.N - k0);
-    const __amdgpu_buffer_rsrc_t rs =
-        make_rsrc(shead + (int64_t)wrow0 * p.ss2 + k0,
-                  __builtin_amdgcn_readfirstlane(
-                      nrows > 0 && nkeys > 0
-                          ? (uint32_t)(((int64_t)(nrows - 1) * p.ss2 + nkeys) * 2)
-                          : 0u));
     const int u = lane & 7;
+    if constexpr (GROUP) {
+      // Row v = wrow0 + r is position (wrow0 >> pshift) + (r >> pshift) of
+      // head h0 + (r & (2^pshift - 1)) (wrow0 is a multiple of 32), so the
+      // lane offsets from the step's first position are the same in every
+      // step; the host bounds every valid offset below kScoresGroupBytes.
+      const int m0 = wrow0 >> p.pshift;
+      const __amdgpu_buffer_rsrc_t rs =
+          make_rsrc(shead + (int64_t)m0 * p.ss2 + k0, kScoresGroupBytes);
+      const int jm = (1 << p.pshift) - 1;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = (lane >> 3) + 8 * i;
-      const u32x4 val = st[r * 8 + (u ^ ((r >> 1) & 7))];
-      buf_store16_nt(val, rs, key_ok ? (uint32_t)((r * p.ss2 + 8 * u) * 2) : kOffNoneScores);
+      for (int i = 0; i < 4; ++i) {
+        const int r = (lane >> 3) + 8 * i, mr = r >> p.pshift;
+        const u32x4 val = st[r * 8 + (u ^ ((r >> 1) & 7))];
+        buf_store16_nt(val, rs,
+                       key_ok && m0 + mr < p.M
+                           ? (uint32_t)(((r & jm) * p.ss1 + mr * p.ss2 + 8 * u) * 2)
+                           : kOffNoneScores);
+      }
+    } else {
+      // The buffer ends at the wave's last key below N in its last row below
+      // M (row stride >= N), so stores to rows past M drop out.
+      const int nrows = min(32, p.M - wrow0), nkeys = min(64, p.N - k0);
+      const __amdgpu_buffer_rsrc_t rs =
+          make_rsrc(shead + (int64_t)wrow0 * p.ss2 + k0,
+                    __builtin_amdgcn_readfirstlane(
+                        nrows > 0 && nkeys > 0
+                            ? (uint32_t)(((int64_t)(nrows - 1) * p.ss2 + nkeys) * 2)
+                            : 0u));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = (lane >> 3) + 8 * i;
+        const u32x4 val = st[r * 8 + (u ^ ((r >> 1) & 7))];
+        buf_store16_nt(val, rs, key_ok ? (uint32_t)((r * p.ss2 + 8 * u) * 2) : kOffNoneScores);
+      }
     }
   } else if (!VEC_ONLY && row < p.M) {
     uint16_t* sr = shead + (int64_t)row * p.ss2;
@@ -247,7 +274,10 @@ void scores_kernel(const ScoresParams p) {
 // block before it runs, so the K loads overlap that block's score stores;
 // between blocks no Q is loaded and no barrier is taken.  The workgroups of
 // a head that run at once write neighbouring key blocks of the same rows.
-// ROWS (32, 64, 128 or 256, the fewest that cover M) rows are resident.
+// Under GQA a workgroup serves 2^pshift query heads of one KV head (their
+// rows interleaved, 2^pshift * M <= 256), so their K is loaded once.
+// ROWS (32, 64, 128 or 256, the fewest that cover 2^pshift * M) rows are
+// resident.
 // The 8 waves are 8 key groups of 64 keys (512-key blocks) that run the
 // block's rows in steps of 32: every wave loads its keys once, where row
 // groups of one key group would each load them (M = 32 with two row groups
@@ -272,20 +302,22 @@ void scores_qres_kernel(const ScoresParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, c = lane & 31, g = lane >> 5;
   const int kg = wave;  // the wave's key group
-  // A head has ngrp workgroups; XCD assignment as in scores_kernel.
-  int w, bh;
+  // A head group has ngrp workgroups; XCD assignment as in scores_kernel,
+  // over the B * H / 2^pshift groups.
+  int w, bg;
   {
-    const int bid = blockIdx.x, heads = p.B * p.H;
-    if ((heads & 7) == 0) {
-      const int per = heads >> 3, x = bid & 7, sidx = bid >> 3;
-      bh = x * per + sidx / p.ngrp;
+    const int bid = blockIdx.x, groups = (p.B * p.H) >> p.pshift;
+    if ((groups & 7) == 0) {
+      const int per = groups >> 3, x = bid & 7, sidx = bid >> 3;
+      bg = x * per + sidx / p.ngrp;
       w = sidx % p.ngrp;
     } else {
-      bh = bid / p.ngrp;
+      bg = bid / p.ngrp;
       w = bid % p.ngrp;
     }
   }
-  const int b = bh / p.H, h = bh % p.H, hk = h / p.G;
+  const int hg = p.H >> p.pshift;  // groups per batch entry
+  const int b = bg / hg, h = (bg % hg) << p.pshift, hk = h / p.G;  // h: the group's first head
   uint16_t* const shead = p.scores + b * p.ss0 + h * p.ss1;
   u32x4* const st = stg[wave];
   const uint16_t* const kbase = p.k + b * p.sk0 + hk * p.sk1;
@@ -298,15 +330,19 @@ void scores_qres_kernel(const ScoresParams p) {
   u32x4 a0[KS], a1[KS], b0[KS], b1[KS];
   scores_load_keys<D>(a0, a1, rk, KPB * w + 64 * kg, p.sk2, c, g);
   {
-    // Q rows [0, ROWS): chunk tid + 512 i is (row, 16-byte chunk ch); rows
-    // past M read as zeros.
+    // Virtual rows [0, ROWS): chunk tid + 512 i is (row v, 16-byte chunk
+    // ch), v holding position v >> pshift of head h + (v & (2^pshift - 1));
+    // positions past M read as zeros.
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(p.q + b * p.sq0 + h * p.sq1, p.q_bytes);
+    const int jm = (1 << p.pshift) - 1;
     u32x4 qst[CPT];
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int id = tid + 64 * kScoresWaves * i, row = id / CPR, ch = id % CPR;
+      const int m = row >> p.pshift;
       if (QCH % (64 * kScoresWaves) == 0 || id < QCH)
-        qst[i] = buf_load16(rq, (uint32_t)((row * p.sq2 + ch * 8) * 2));
+        qst[i] = buf_load16(rq, m < p.M ? (uint32_t)(((row & jm) * p.sq1 + m * p.sq2 + ch * 8) * 2)
+                                        : kOffNoneScores);
     }
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
@@ -329,7 +365,8 @@ void scores_qres_kernel(const ScoresParams p) {
     const int k0 = KPB * kb + 64 * kg;  // the wave's first key
 #pragma unroll
     for (int t = 0; t < NST; ++t)
-      scores_tile<E, D, MASK, true>(p, qtile + 32 * D * t, 0, x0, x1, st, shead, 32 * t, k0, lane);
+      scores_tile<E, D, MASK, true, true>(p, qtile + 32 * D * t, 0, x0, x1, st, shead, 32 * t, k0,
+                                          lane);
   };
   auto load = [&](u32x4(&x0)[KS], u32x4(&x1)[KS], int kb) __attribute__((always_inline)) {
     scores_load_keys<D>(x0, x1, kb < p.nkb ? rk : rk_none, KPB * kb + 64 * kg, p.sk2, c, g);

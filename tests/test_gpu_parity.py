@@ -334,7 +334,19 @@ RESIDENT_Q_SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES, ids=_label)
+# GQA: a workgroup serves the largest power-of-two share of a KV head's
+# query heads whose rows fit in 256 (2, 4 and 8 heads: 128, 32 and 192
+# rows, including M = 1), or one head when the group size is odd (7).
+RESIDENT_Q_GROUP_SHAPES = [
+    (1, 32, 8, 32, 32768, 128),
+    (8, 32, 8, 1, 8192, 128),
+    (1, 16, 2, 24, 131072, 64),
+    (1, 28, 4, 16, 32768, 128),
+    (1, 16, 8, 100, 32768, 128),
+]
+
+
+@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES + RESIDENT_Q_GROUP_SHAPES, ids=_label)
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 def test_compute_attention_scores_resident_q(shape, dtype, gpu):
     from flash_attn_with_score_amd.attention_scores import compute_attention_scores
@@ -353,7 +365,7 @@ def test_compute_attention_scores_resident_q(shape, dtype, gpu):
 # key-split forward for O and the masked scores-only kernel (causal: keys
 # past N - M + row written as 0).
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES[:6], ids=_label)
+@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES[:6] + RESIDENT_Q_GROUP_SHAPES[::2], ids=_label)
 def test_scores_short_query_resident_q(shape, causal, gpu):
     _run("attention_with_scores", shape, torch.float16, causal, gpu, seed=15)
 
