@@ -912,7 +912,7 @@ static int run_scores(const char* fn, const fas_attn_args* a, const Problem& pr,
                   pr.N % 8 == 0
               ? 1
               : 0;
-  // Up to 256 query rows with 16-byte score stores: the resident-Q kernel,
+  // Up to 512 query rows with 16-byte score stores: the resident-Q kernel,
   // one workgroup per CU, each walking two or more of its head's 512-key
   // blocks.
   // Under GQA a workgroup takes the largest power-of-two share of a KV

@@ -29,7 +29,7 @@ hipError_t launch_scores(const ScoresParams& p, int dtype, int d, hipStream_t s)
 constexpr int kScoresKeysPerBlock = 256;
 // Most query rows, and keys per block, of the resident-Q scores kernel
 // (ScoresParams::ngrp > 0).
-constexpr int kScoresResidentRows = 256;
+constexpr int kScoresResidentRows = 512;
 constexpr int kScoresResidentKeys = 512;
 // Bound on the resident-Q kernel's q and score offsets within a head group.
 constexpr int64_t kScoresResidentBytes = 0x7ffffff0;

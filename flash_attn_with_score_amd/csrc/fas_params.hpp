@@ -279,7 +279,7 @@ struct ScoresParams {
   int spr;            // 64-row steps per row range
   int ngrp;           // > 0: resident-Q kernel with ngrp workgroups per head group
   // Resident-Q kernel: a group is 2^pshift consecutive query heads of one KV
-  // head (pshift > 0 only under GQA, 2^pshift * M <= 256), its virtual rows
+  // head (pshift > 0 only under GQA, 2^pshift * M <= 512), its virtual rows
   // v = m * 2^pshift + j holding position m of head h0 + j.
   int pshift;
   int vec;            // base and row strides 16-byte aligned, N % 8 == 0: 16-byte stores

@@ -17,8 +17,10 @@ static void qres_launch(int rows, dim3 g, dim3 b, const ScoresParams& p, hipStre
     hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 64>), g, b, 0, s, p);
   else if (rows == 128)
     hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 128>), g, b, 0, s, p);
-  else
+  else if (rows == 256)
     hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 256>), g, b, 0, s, p);
+  else
+    hipLaunchKernelGGL((scores_qres_kernel<E, D, MASK, 512>), g, b, 0, s, p);
 }
 
 template <class E, int D>
@@ -31,10 +33,10 @@ static hipError_t scores_t(const ScoresParams& p, hipStream_t s) {
     const int64_t grid = ((int64_t)p.B * p.H >> p.pshift) * p.ngrp;
     if (grid > INT32_MAX) return hipErrorInvalidValue;
     const dim3 g((unsigned)grid), b(64 * kScoresWaves);
-    // Resident rows: the fewest of 32, 64, 128 and 256 that cover the
+    // Resident rows: the fewest of 32, 64, 128, 256 and 512 that cover the
     // group's 2^pshift * M rows (nkb counts 512-key blocks).
     const int vr = p.M << p.pshift;
-    const int rows = vr <= 32 ? 32 : vr <= 64 ? 64 : vr <= 128 ? 128 : 256;
+    const int rows = vr <= 32 ? 32 : vr <= 64 ? 64 : vr <= 128 ? 128 : vr <= 256 ? 256 : 512;
     if (p.mask)
       qres_launch<E, D, true>(rows, g, b, p, s);
     else

@@ -25,7 +25,7 @@
 // concurrent 512-byte runs while only a few thousand rows are open over the
 // chip.  Q is read once per key block, K once.
 //
-// Short query ranges (M <= 256) give such a workgroup only a few steps
+// Short query ranges (M <= 512) give such a workgroup only a few steps
 // after its K load, so there scores_qres_kernel keeps the head's Q rows
 // resident in LDS instead and walks several key blocks of the head, the next
 // block's K loaded into a second register set while the current one's steps
@@ -45,7 +45,7 @@ constexpr uint32_t kScoresGroupBytes = 0x7ffffff0u;
 constexpr int kScoresWaves = 8;
 constexpr int kScoresRows = 64;    // query rows per step (2 row groups x 32)
 constexpr int kScoresKeys = 256;   // keys per workgroup (4 key groups x 64)
-constexpr int kScoresResRows = 256;  // query rows resident in scores_qres_kernel
+constexpr int kScoresResRows = 512;  // most query rows resident in scores_qres_kernel
 
 // The wave's 64 keys [k0, k0 + 64) as A operands of S^T = K Q^T (keys past
 // N read as zeros): a0 holds keys k0 + perm_row(c), a1 those 32 above.
@@ -275,20 +275,21 @@ void scores_kernel(const ScoresParams p) {
 // between blocks no Q is loaded and no barrier is taken.  The workgroups of
 // a head that run at once write neighbouring key blocks of the same rows.
 // Under GQA a workgroup serves 2^pshift query heads of one KV head (their
-// rows interleaved, 2^pshift * M <= 256), so their K is loaded once.
-// ROWS (32, 64, 128 or 256, the fewest that cover 2^pshift * M) rows are
-// resident.
+// rows interleaved, 2^pshift * M <= 512), so their K is loaded once.
+// ROWS (32, 64, 128, 256 or 512, the fewest that cover 2^pshift * M) rows
+// are resident.
 // The 8 waves are 8 key groups of 64 keys (512-key blocks) that run the
 // block's rows in steps of 32: every wave loads its keys once, where row
 // groups of one key group would each load them (M = 32 with two row groups
 // of 256-key blocks: 97 against 52 us at B1 H32 N32768), and each step
-// writes 1 KiB runs of 32 rows.  With up to 96 KiB of LDS (D = 128, 256
-// rows) and up to ~240 VGPRs one workgroup (8 waves, two per SIMD) runs
-// per CU.  Whole 16-byte score stores only (p.vec).
+// writes 1 KiB runs of 32 rows.  With up to 160 KiB of LDS (D = 128, 512
+// rows) and up to 256 VGPRs one workgroup (8 waves, two per SIMD) runs per
+// CU.  Whole 16-byte score stores only (p.vec).
 template <class E, int D, bool MASK, int ROWS>
 __global__ __launch_bounds__(64 * kScoresWaves) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void scores_qres_kernel(const ScoresParams p) {
-  static_assert(ROWS == 32 || ROWS == 64 || ROWS == 128 || ROWS == 256, "resident rows");
+  static_assert(ROWS == 32 || ROWS == 64 || ROWS == 128 || ROWS == 256 || ROWS == 512,
+                "resident rows");
   constexpr int KS = D / 16;
   constexpr int KPB = 64 * kScoresWaves;                // keys per block
   constexpr int NST = ROWS / 32;                        // steps of 32 rows per block
@@ -363,7 +364,9 @@ void scores_qres_kernel(const ScoresParams p) {
   auto block = [&](const u32x4(&x0)[KS], const u32x4(&x1)[KS], int kb)
                    __attribute__((always_inline)) {
     const int k0 = KPB * kb + 64 * kg;  // the wave's first key
-#pragma unroll
+    // Up to 8 steps unrolled (512 rows: a loop of two, which keeps the
+    // 256-VGPR budget).
+#pragma unroll 8
     for (int t = 0; t < NST; ++t)
       scores_tile<E, D, MASK, true, true>(p, qtile + 32 * D * t, 0, x0, x1, st, shead, 32 * t, k0,
                                           lane);

@@ -314,16 +314,17 @@ def test_compute_attention_scores(shape, dtype, gpu):
 
 
 
-# Short query ranges (M <= 256) over many key blocks: the scores-only
-# kernel keeps each head's Q rows in LDS (32, 64, 128 or 256 rows) and every
-# workgroup walks several 512-key blocks (16-byte stores only).  B*H a
-# multiple of 8 and not (12 heads), GQA, a partial last key block and last
-# step, M = 1, uneven numbers of blocks per workgroup (20 blocks over 8
+# Short query ranges (M <= 512) over many key blocks: the scores-only
+# kernel keeps each head group's Q rows in LDS (32, 64, 128, 256 or 512
+# rows) and every workgroup walks several 512-key blocks (16-byte stores
+# only).  B*H a multiple of 8 and not (12 heads), GQA (two heads of a group
+# of 4 per workgroup at M = 200), a partial last key block and last step,
+# M = 1, uneven numbers of blocks per workgroup (34 blocks over 16
 # workgroups), and B*H >= 256 (one workgroup per head, 2-4 blocks each) at
 # D 16 to 128.
 RESIDENT_Q_SHAPES = [
     (1, 32, 32, 256, 8192, 128),
-    (2, 16, 4, 200, 10000, 64),
+    (2, 16, 4, 200, 17000, 64),
     (1, 12, 12, 37, 22600, 128),
     (1, 16, 8, 100, 16384, 128),
     (1, 32, 32, 32, 8200, 128),
@@ -331,11 +332,13 @@ RESIDENT_Q_SHAPES = [
     (8, 32, 8, 1, 2048, 128),
     (4, 64, 64, 64, 520, 32),
     (2, 128, 128, 130, 1800, 16),
+    (1, 32, 32, 512, 8192, 128),
+    (1, 16, 16, 300, 16384, 64),
 ]
 
 
 # GQA: a workgroup serves the largest power-of-two share of a KV head's
-# query heads whose rows fit in 256 (2, 4 and 8 heads: 128, 32 and 192
+# query heads whose rows fit in 512 (2, 4 and 8 heads: 200, 128 and 192
 # rows, including M = 1), or one head when the group size is odd (7).
 RESIDENT_Q_GROUP_SHAPES = [
     (1, 32, 8, 32, 32768, 128),
@@ -365,7 +368,8 @@ def test_compute_attention_scores_resident_q(shape, dtype, gpu):
 # key-split forward for O and the masked scores-only kernel (causal: keys
 # past N - M + row written as 0).
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES[:6] + RESIDENT_Q_GROUP_SHAPES[::2], ids=_label)
+@pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES[:6] + RESIDENT_Q_SHAPES[9:] +
+                         RESIDENT_Q_GROUP_SHAPES[::2], ids=_label)
 def test_scores_short_query_resident_q(shape, causal, gpu):
     _run("attention_with_scores", shape, torch.float16, causal, gpu, seed=15)
 
