@@ -389,10 +389,17 @@ struct Workspace {
 // ranges against long key ranges: decode, last-window scoring), each row
 // block's key tiles are dealt to nsplit workgroups of at least 8 tiles,
 // aiming at ~512 workgroups in all.  Depends on sizes only, so the workspace
-// query and the launch agree.  The scores variant splits only below 64 row
-// blocks: its split route writes the scores in a second kernel, which the
-// fused writer beats while it still has a quarter of the CUs busy.
+// query and the launch agree.  The scores variant splits only up to 64 row
+// blocks, or 128 when the key range is at least 8 times the query range:
+// its split route writes the scores in a second kernel, which the fused
+// writer beats while it still has a quarter of the CUs busy, or half of
+// them over keys not much longer than its rows (B2 H32 M512 N16384: 0.607
+// against 0.734 ms fused; B1 H32 M1024 N16384: 0.547 against 0.592; B1 H32
+// M = N = 1024 stays fused).
 constexpr int64_t kScoresSplitMaxWgs = 64;
+static int64_t scores_split_max_wgs(const Problem& pr) {
+  return pr.N >= 8 * (int64_t)pr.M ? 2 * kScoresSplitMaxWgs : kScoresSplitMaxWgs;
+}
 // Bytes of the fp32 partials of a plan (O, offset, weight sum, row sum).
 size_t split_bytes(const Problem& pr, const SplitPlan& sp) {
   const size_t rows = (size_t)pr.B * pr.H * sp.nsplit * sp.mpad;
@@ -615,7 +622,7 @@ Workspace layout(int variant, const Problem& pr, int64_t split, size_t budget = 
   }
   if (forward_can_split(variant) && off <= budget) {
     const SplitPlan sp = split_plan(pr, variant == FAS_VARIANT_CROSS_QK_SUM,
-                                    variant == FAS_VARIANT_SCORES ? kScoresSplitMaxWgs : 255,
+                                    variant == FAS_VARIANT_SCORES ? scores_split_max_wgs(pr) : 255,
                                     budget - off);
     if (sp.nsplit > 1) {
       const size_t rows = (size_t)pr.B * pr.H * sp.nsplit * sp.mpad;
