@@ -390,15 +390,19 @@ struct Workspace {
 // block's key tiles are dealt to nsplit workgroups of at least 8 tiles,
 // aiming at ~512 workgroups in all.  Depends on sizes only, so the workspace
 // query and the launch agree.  The scores variant splits only up to 64 row
-// blocks, or 128 when the key range is at least 8 times the query range:
-// its split route writes the scores in a second kernel, which the fused
-// writer beats while it still has a quarter of the CUs busy, or half of
-// them over keys not much longer than its rows (B2 H32 M512 N16384: 0.607
-// against 0.734 ms fused; B1 H32 M1024 N16384: 0.547 against 0.592; B1 H32
-// M = N = 1024 stays fused).
+// blocks, 128 when the key range is at least 8 times the query range, 256
+// at 64 times: its split route writes the scores in a second kernel, which
+// the fused writer beats while it still has a quarter of the CUs busy, or
+// half or all of them over keys not much longer than its rows (B2 H32 M512
+// N16384: 0.607 against 0.734 ms fused; B1 H32 M1024 N16384: 0.547 against
+// 0.592; B8 H32 M256 N16384: 1.27 against 1.58; but B4 H32 M512 N16384:
+// 1.19 against 1.16 fused; B1 H32 M = N = 1024 stays fused).
 constexpr int64_t kScoresSplitMaxWgs = 64;
 static int64_t scores_split_max_wgs(const Problem& pr) {
-  return pr.N >= 8 * (int64_t)pr.M ? 2 * kScoresSplitMaxWgs : kScoresSplitMaxWgs;
+  const int64_t m = pr.M;
+  return pr.N >= 64 * m ? 4 * kScoresSplitMaxWgs
+         : pr.N >= 8 * m ? 2 * kScoresSplitMaxWgs
+                         : kScoresSplitMaxWgs;
 }
 // Bytes of the fp32 partials of a plan (O, offset, weight sum, row sum).
 size_t split_bytes(const Problem& pr, const SplitPlan& sp) {

@@ -368,9 +368,11 @@ def test_compute_attention_scores_resident_q(shape, dtype, gpu):
 # key-split forward for O and the masked scores-only kernel (causal: keys
 # past N - M + row written as 0).
 @pytest.mark.parametrize("causal", [False, True], ids=["full", "causal"])
-# (2, 32, 32, 300, 4096, 64): 128 row blocks with N >= 8 M, also split.
+# (2, 32, 32, 300, 4096, 64): 128 row blocks with N >= 8 M, also split;
+# (8, 32, 32, 40, 2600, 32): 256 row blocks of M = 40, split at N >= 64 M.
 @pytest.mark.parametrize("shape", RESIDENT_Q_SHAPES[:6] + RESIDENT_Q_SHAPES[9:] +
-                         RESIDENT_Q_GROUP_SHAPES[::2] + [(2, 32, 32, 300, 4096, 64)],
+                         RESIDENT_Q_GROUP_SHAPES[::2] +
+                         [(2, 32, 32, 300, 4096, 64), (8, 32, 32, 40, 2600, 32)],
                          ids=_label)
 def test_scores_short_query_resident_q(shape, causal, gpu):
     _run("attention_with_scores", shape, torch.float16, causal, gpu, seed=15)
